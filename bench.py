@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Benchmark of the fp32 GRU training step (forward + backward) on one MI355X.
+
+Workload = BASELINE config 2: 1-layer GRU, input 256, hidden 256, batch 64,
+seq_len 512, fp32; x ~ N(0,1), PyTorch-uniform init, h0 ~ 0.1 N(0,1), MSE loss
+against an N(0,1) target; a step is forward + loss + backward producing the
+gradients of all four weight/bias tensors, x and h0 (no optimizer, as the
+reference's published fwd+bwd numbers).  Inputs are generated on the CPU with
+seed 42, copied to the GPU, and resident in HBM before timing starts.
+
+Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
+  roofline      - the dominant kernel's achieved vs peak rate, from the
+                  library's own per-stage hipEvent timing of the timed steps;
+  cpu_baseline  - the C oracle (fp32, one thread) on a bounded sample of the
+                  same workload (fewer timesteps), timed on this host;
+  torch_gru_gpu - torch.nn.GRU (MIOpen/rocBLAS) on the same GPU, same protocol;
+  torch_gru_cpu - torch.nn.GRU on this host's CPU cores, bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "fp32 GRU fwd+bwd timesteps/sec & µs/step, H=256 B=64 T=512, 1 MI355X"
+B, T, I, H, L = 64, 512, 256, 256, 1
+SEED = 42
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+
+def flops_per_step(B, T, I, H):
+    # 2*B*T*3H*(I+H) forward + backward (dh, dW_hh, dx, dW_ih): 18*B*T*H*(I+H).
+    return 18.0 * B * T * H * (I + H)
+
+
+def stage_flops(B, T, I, H):
+    return {
+        "input_gemm": 2.0 * B * T * 3 * H * I,
+        "forward_recurrence": 2.0 * B * T * 3 * H * H,
+        "backward_recurrence": 2.0 * B * T * 3 * H * H,
+        "dw_hh_gemm": 2.0 * B * T * 3 * H * H,
+        "dw_ih_gemm": 2.0 * B * T * 3 * H * I,
+        "dx_gemm": 2.0 * B * T * 3 * H * I,
+    }
+
+
+def make_inputs():
+    import torch
+
+    torch.manual_seed(SEED)
+    gru = torch.nn.GRU(I, H, num_layers=L, batch_first=True)  # PyTorch-uniform init
+    x = torch.randn(B, T, I)
+    h0 = 0.1 * torch.randn(L, B, H)
+    target = torch.randn(B, T, H)
+    return gru, x, h0, target
+
+
+def time_steps(model, x, h0, target, steps, warmup, sync, profile_cb=None):
+    import torch
+    import torch.nn.functional as F
+
+    def step():
+        for p in model.parameters():
+            p.grad = None
+        x.grad = None
+        h0.grad = None
+        out, hn = model(x, h0)
+        loss = F.mse_loss(out, target)
+        loss.backward()
+
+    for _ in range(warmup):
+        step()
+    sync()
+    if profile_cb:
+        profile_cb(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sync()
+    elapsed = time.perf_counter() - t0
+    return elapsed / steps
+
+
+def cpu_oracle_baseline(budget_s: float):
+    """C oracle (fp32, single thread) on the c2 shape with fewer timesteps."""
+    import numpy as np
+    from oracle import gru_oracle
+
+    gru_oracle.build()
+    gru, x, h0, target = make_inputs()
+    p = {n: getattr(gru, f"{n}_l0").detach().numpy() for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")}
+    t_sample = 8
+    while True:
+        xs = x[:, :t_sample].numpy()
+        t0 = time.perf_counter()
+        f = gru_oracle.forward(xs, h0[0].numpy(), p["weight_ih"], p["weight_hh"], p["bias_ih"], p["bias_hh"],
+                               dtype=np.float32)
+        dy = (2.0 / (B * t_sample * H)) * (f.y - target[:, :t_sample].numpy())
+        gru_oracle.backward(xs, h0[0].numpy(), p["weight_ih"], p["weight_hh"], f.y, f.cache, dy, None,
+                            dtype=np.float32)
+        dt = time.perf_counter() - t0
+        if dt * 4 > budget_s or t_sample >= T:
+            break
+        t_sample = min(T, t_sample * 4)
+    return {
+        "value": t_sample / dt,
+        "unit": "timesteps/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"C oracle fp32 fwd+bwd, B={B} I={I} H={H}, T={t_sample} of {T} timesteps, {dt:.2f} s",
+    }
+
+
+def torch_cpu_baseline(budget_s: float):
+    import torch
+    import torch.nn.functional as F
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    gru, x, h0, target = make_inputs()
+    t_sample = 16
+    while True:
+        xs = x[:, :t_sample].clone().requires_grad_(True)
+        hs = h0.clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        out, _ = gru(xs, hs)
+        F.mse_loss(out, target[:, :t_sample]).backward()
+        dt = time.perf_counter() - t0
+        if dt * 4 > budget_s or t_sample >= T:
+            break
+        t_sample = min(T, t_sample * 4)
+    return {"value": t_sample / dt, "unit": "timesteps/s", "threads": threads,
+            "sample": f"torch.nn.GRU fp32 CPU fwd+bwd, T={t_sample} of {T}, {dt:.2f} s"}
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds per CPU baseline sample")
+    parser.add_argument("--skip-cpu", action="store_true")
+    parser.add_argument("--skip-torch-gpu", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path is single-GPU "
+              "and its data-parallel sharding is a design note, not a measured configuration.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from rnn_kernel_amd import _lib, from_torch_gru
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    sync = torch.cuda.synchronize
+
+    gru, x_cpu, h0_cpu, target_cpu = make_inputs()
+    x = x_cpu.to(dev).requires_grad_(True)
+    h0 = h0_cpu.to(dev).requires_grad_(True)
+    target = target_cpu.to(dev)
+    ours = from_torch_gru(gru.to(dev))
+
+    _lib.profile_read()  # clear
+    t_step = time_steps(ours, x, h0, target, args.steps, args.warmup, sync, profile_cb=_lib.profile_enable)
+    stages = _lib.profile_read()
+    _lib.profile_enable(False)
+    # second timed pass without event records for the headline number
+    t_step_noprof = time_steps(ours, x, h0, target, args.steps, 0, sync)
+    t_step = min(t_step, t_step_noprof)
+
+    flops = stage_flops(B, T, I, H)
+    stage_avg = {k: (ms / n if n else 0.0) for k, (ms, n) in stages.items()}
+    dominant = max(stage_avg, key=stage_avg.get)
+    dom_ms = stage_avg[dominant]
+    achieved = flops[dominant] / (dom_ms * 1e-3) / 1e12 if dom_ms > 0 else 0.0
+
+    result = {
+        "metric": METRIC,
+        "value": T / t_step,
+        "unit": "timesteps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": t_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seed 42, CPU-generated, PyTorch-uniform init)",
+        "config": {"workload": "BASELINE config 2: 1-layer GRU fwd+bwd, MSE loss, no optimizer",
+                   "batch": B, "seq_len": T, "input_size": I, "hidden_size": H, "layers": L},
+        "us_per_timestep": t_step * 1e6 / T,
+        "tokens_per_s": B * T / t_step,
+        "step_tflops": flops_per_step(B, T, I, H) / t_step / 1e12,
+        "stages_ms": {k: round(v, 4) for k, v in stage_avg.items()},
+        "roofline": {
+            "kernel": dominant,
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": MFMA_FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
+            "traffic": None,
+            "note": "serial recurrence: latency-bound; achieved = algorithmic FLOPs / measured duration",
+            "us_per_timestep": dom_ms * 1e3 / T,
+        },
+    }
+
+    if not args.skip_torch_gpu:
+        gru_gpu = gru.to(dev)
+        gru_gpu.flatten_parameters()
+        x.grad = None
+        t_torch = time_steps(gru_gpu, x, h0, target, max(3, args.steps // 2), 2, sync)
+        result["torch_gru_gpu"] = {"value": T / t_torch, "unit": "timesteps/s", "ms_per_step": t_torch * 1e3,
+                                   "speedup_of_ours": t_torch / t_step}
+    if not args.skip_cpu:
+        result["cpu_baseline"] = cpu_oracle_baseline(args.cpu_budget)
+        result["torch_gru_cpu"] = torch_cpu_baseline(args.cpu_budget)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

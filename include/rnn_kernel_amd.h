@@ -1,0 +1,170 @@
+/*
+ * rnn_kernel_amd — C ABI of the MI355X (gfx950) fp32 GRU training path.
+ *
+ * Conventions for every entry point:
+ *   - all pointers are device pointers owned by the caller (PyTorch's caching
+ *     allocator in the Python front end); the library never allocates device
+ *     memory in these calls;
+ *   - work is enqueued on `stream` (a hipStream_t, NULL = default stream) and
+ *     is asynchronous: no host synchronisation happens inside;
+ *   - the device is the calling thread's current HIP device;
+ *   - the return value is 0 on success, otherwise a nonzero code; the message
+ *     of the last failure on the calling thread is rka_last_error();
+ *   - tensors are dense row-major fp32: x [B,T,I], y/dy [B,T,H] (batch
+ *     first), h0/hn/dh0 [B,H], W_ih [3H,I], W_hh [3H,H], biases [3H], with
+ *     nn.GRU's gate order r, z, n in row blocks [0,H), [H,2H), [2H,3H).
+ *
+ * The reference binds its kernels from Python with cuda-python
+ * (cuLaunchCooperativeKernel on raw pointers, torch's current stream);
+ * each entry point below names the reference launcher it replaces.
+ */
+#ifndef RNN_KERNEL_AMD_H
+#define RNN_KERNEL_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes (besides hipError_t values passed through). */
+#define RKA_OK 0
+#define RKA_ERR_INVALID_ARGUMENT 1001
+#define RKA_ERR_WORKSPACE_TOO_SMALL 1002
+#define RKA_ERR_UNSUPPORTED_DEVICE 1003
+#define RKA_ERR_UNSUPPORTED_SHAPE 1004
+#define RKA_ERR_TOO_LARGE_FOR_RESIDENT_LAUNCH 1005
+
+/* Library ABI version. */
+int rka_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* rka_last_error(void);
+
+/* 1 if `device` is a gfx950 (MI355X-class) GPU this library was built for,
+ * 0 otherwise (message in rka_last_error()).  Replaces the reference's
+ * _validate_a100_device / is_a100_available capability checks
+ * (src/rnn_kernel/a100/prod/gru.py:109-117,139-148). */
+int rka_device_supported(int device);
+
+/* Bytes of the per-layer gate cache ("reserve": r, z, n, a_n per unit and
+ * step) that rka_gru_forward writes in training mode and rka_gru_backward
+ * reads.  Replaces the reference's gate_cache [B,T,4H] allocation
+ * (src/rnn_kernel/a100/prod/gru.py:238). */
+size_t rka_gru_reserve_bytes(int batch, int seq_len, int hidden_size);
+
+/* Workspace bytes rka_gru_forward needs (input-gate buffer, exchange
+ * buffers, flags). */
+size_t rka_gru_forward_workspace_bytes(int batch, int seq_len, int input_size, int hidden_size);
+
+/*
+ * Forward of one GRU layer: input projection (fp32 MFMA GEMM) followed by the
+ * persistent recurrence.  Writes y [B,T,H] and hn [B,H].  When `reserve` is
+ * non-NULL (training) it also writes the gate cache there; when NULL
+ * (inference) no cache is written.
+ * Replaces F.linear + _launch_forward / _launch_forward_no_cache + the h_n
+ * copy (src/rnn_kernel/a100/prod/gru.py:519-525,226-376,610-616).
+ */
+int rka_gru_forward(const float* x, const float* h0,
+                    const float* w_ih, const float* w_hh,
+                    const float* b_ih, const float* b_hh,
+                    float* y, float* hn, float* reserve,
+                    void* workspace, size_t workspace_bytes,
+                    int batch, int seq_len, int input_size, int hidden_size,
+                    void* stream);
+
+/* Workspace bytes rka_gru_backward needs (gate-gradient buffer, exchange
+ * buffers, split-K partials, flags). */
+size_t rka_gru_backward_workspace_bytes(int batch, int seq_len, int input_size, int hidden_size);
+
+/*
+ * Backward of one GRU layer from the forward's y and reserve.
+ * dy [B,T,H] may be NULL (zeros, gru.py:534-535); dhn [B,H] may be NULL (no
+ * gradient on h_n, gru.py:552-554); dx may be NULL (input gradient not
+ * needed).  Writes (does not accumulate) dx, dh0, dw_ih, dw_hh, db_ih, db_hh.
+ * Replaces _launch_pack_hidden_prev + _launch_backward_sequence + the cuBLAS
+ * gradient GEMMs (src/rnn_kernel/a100/prod/gru.py:531-580,379-487).
+ */
+int rka_gru_backward(const float* x, const float* h0,
+                     const float* w_ih, const float* w_hh,
+                     const float* y, const float* reserve,
+                     const float* dy, const float* dhn,
+                     float* dx, float* dh0,
+                     float* dw_ih, float* dw_hh, float* db_ih, float* db_hh,
+                     void* workspace, size_t workspace_bytes,
+                     int batch, int seq_len, int input_size, int hidden_size,
+                     void* stream);
+
+/*
+ * Building blocks (each is a stage of the two calls above, exported for
+ * kernel-level parity tests and profiling).
+ */
+
+/* C[m,n] = sum_k A(m,k) B(n,k) (+ bias[n] if bias != NULL), fp32 MFMA.
+ * A(m,k) = a[m*lda+k] if a_kmajor == 0 else a[k*lda+m];
+ * B(n,k) = b[n*ldb+k] if b_kmajor == 0 else b[k*ldb+n].
+ * Replaces the torch F.linear / matmul calls of gru.py:519-523,571-578. */
+int rka_gemm_f32(int m, int n, int k,
+                 const float* a, int lda, int a_kmajor,
+                 const float* b, int ldb, int b_kmajor,
+                 const float* bias, float* c, int ldc, void* stream);
+
+/* Workspace bytes of the recurrence-only calls below. */
+size_t rka_gru_recurrence_workspace_bytes(int batch, int hidden_size);
+
+/* Persistent forward recurrence from precomputed input gates gx [B,T,3H]
+ * (x W_ih^T + b_ih).  Writes y, hn and (if non-NULL) the reserve.
+ * Replaces _launch_forward / _launch_forward_no_cache
+ * (src/rnn_kernel/a100/prod/gru.py:226-376). */
+int rka_gru_recurrence_forward(const float* gx, const float* h0,
+                               const float* w_hh, const float* b_hh,
+                               float* y, float* hn, float* reserve,
+                               void* workspace, size_t workspace_bytes,
+                               int batch, int seq_len, int hidden_size,
+                               void* stream);
+
+/* Persistent reverse-time recurrence.  Writes the gate gradients
+ * g [B,T,4H] as blocks (da_n, dr^, dz^, dn^) and dh0.  dy / dhn may be NULL.
+ * Replaces _launch_backward_sequence (src/rnn_kernel/a100/prod/gru.py:415-487),
+ * whose G_i / G_h outputs are the column ranges [H,4H) and the rotation of
+ * [0,3H) of g. */
+int rka_gru_recurrence_backward(const float* dy, const float* dhn,
+                                const float* reserve, const float* h0,
+                                const float* y, const float* w_hh,
+                                float* g, float* dh0,
+                                void* workspace, size_t workspace_bytes,
+                                int batch, int seq_len, int hidden_size,
+                                void* stream);
+
+/* Override the recurrence work decomposition (0 = automatic choice).
+ * units: hidden units per workgroup (a divisor of 64);
+ * pair_waves: wavefronts holding (row, unit) pairs (1, 2 or 4).
+ * Affects later calls on all threads.  For tuning and tests. */
+int rka_set_recurrence_config(int fwd_units, int fwd_pair_waves,
+                              int bwd_units, int bwd_pair_waves);
+
+/* Describe the decomposition the next recurrence call would use for this
+ * shape: writes {groups, slices, units, rows_per_group, pair_waves,
+ * lds_bytes} for the forward (dir=0) or backward (dir=1) kernel. */
+int rka_describe_recurrence(int dir, int batch, int hidden_size, int out6[6]);
+
+
+/*
+ * Stage profiler (the native counterpart of the reference's per-phase CUDA
+ * events, rnn_benchmark.py:642-694).  While enabled, every stage launch of
+ * rka_gru_forward / rka_gru_backward is bracketed by a pair of hipEvents on
+ * its stream; rka_profile_read() waits for the recorded events, returns the
+ * summed milliseconds and launch counts per stage and clears the records.
+ * Stage ids: 0 input GEMM, 1 forward recurrence, 2 backward recurrence,
+ * 3 dW_hh GEMM (+reduction), 4 dW_ih GEMM (+reduction), 5 dx GEMM.
+ */
+#define RKA_NUM_STAGES 6
+int rka_profile_enable(int on);
+int rka_profile_read(double ms_out[RKA_NUM_STAGES], int count_out[RKA_NUM_STAGES]);
+const char* rka_profile_stage_name(int stage);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RNN_KERNEL_AMD_H */

@@ -1,0 +1,170 @@
+"""numpy front end of the C GRU oracle.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module; the product
+package ``rnn_kernel_amd`` never does.  It is the checker the HIP path is
+compared against, never a fallback for it.
+
+The arithmetic lives in ``gru_oracle_impl.h`` (a scalar C restatement of the
+reference's forward recurrence, gate cache, BPTT and gradient GEMMs, with
+file:line citations there).  This module adds:
+
+* ``forward`` / ``backward`` for one layer (fp64 or fp32);
+* ``stack_forward_backward`` for a stack of layers with the reference's layer
+  composition (layer l's input is layer l-1's output, ``hx`` sliced per
+  layer, zeros when ``hx`` is None): src/rnn_kernel/a100/prod/gru.py:673-728.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_DIR, "liboracle_gru.so")
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with the committed Makefile (gcc)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _DIR] + (["-B"] if force else []), check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        build()
+    lib = ctypes.CDLL(_LIB_PATH)
+    for suffix in ("_f64", "_f32"):
+        fwd = getattr(lib, "oracle_gru_forward" + suffix)
+        fwd.restype = ctypes.c_int
+        fwd.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 9
+        bwd = getattr(lib, "oracle_gru_backward" + suffix)
+        bwd.restype = ctypes.c_int
+        bwd.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 14
+    _lib = lib
+    return lib
+
+
+def _suffix(dtype) -> str:
+    dtype = np.dtype(dtype)
+    if dtype == np.float64:
+        return "_f64"
+    if dtype == np.float32:
+        return "_f32"
+    raise TypeError(f"oracle supports float32/float64, got {dtype}")
+
+
+def _c(a: Optional[np.ndarray], dtype) -> Optional[np.ndarray]:
+    if a is None:
+        return None
+    return np.ascontiguousarray(np.asarray(a, dtype=dtype))
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+@dataclass
+class ForwardResult:
+    y: np.ndarray       # [B, T, H]
+    hn: np.ndarray      # [B, H]
+    cache: Optional[np.ndarray]  # [B, T, 4H] = (r, z, n, a_n)
+
+
+@dataclass
+class BackwardResult:
+    dx: Optional[np.ndarray]
+    dh0: np.ndarray
+    dw_ih: np.ndarray
+    dw_hh: np.ndarray
+    db_ih: np.ndarray
+    db_hh: np.ndarray
+
+
+def forward(x, h0, w_ih, w_hh, b_ih, b_hh, dtype=np.float64, with_cache: bool = True) -> ForwardResult:
+    """One layer forward; x [B,T,I], h0 [B,H], weights in nn.GRU layout."""
+    lib = _load()
+    x, h0, w_ih, w_hh, b_ih, b_hh = (_c(a, dtype) for a in (x, h0, w_ih, w_hh, b_ih, b_hh))
+    B, T, I = x.shape
+    H = h0.shape[1]
+    assert h0.shape == (B, H) and w_ih.shape == (3 * H, I) and w_hh.shape == (3 * H, H)
+    assert b_ih.shape == (3 * H,) and b_hh.shape == (3 * H,)
+    y = np.empty((B, T, H), dtype=dtype)
+    hn = np.empty((B, H), dtype=dtype)
+    cache = np.empty((B, T, 4 * H), dtype=dtype) if with_cache else None
+    rc = getattr(lib, "oracle_gru_forward" + _suffix(dtype))(
+        B, T, I, H, _p(x), _p(h0), _p(w_ih), _p(w_hh), _p(b_ih), _p(b_hh), _p(y), _p(hn), _p(cache))
+    if rc != 0:
+        raise MemoryError("oracle_gru_forward failed to allocate")
+    return ForwardResult(y, hn, cache)
+
+
+def backward(x, h0, w_ih, w_hh, y, cache, dy, dhn, dtype=np.float64, need_dx: bool = True) -> BackwardResult:
+    """One layer backward from the forward's y and cache; dy/dhn may be None."""
+    lib = _load()
+    x, h0, w_ih, w_hh, y, cache, dy, dhn = (_c(a, dtype) for a in (x, h0, w_ih, w_hh, y, cache, dy, dhn))
+    B, T, I = x.shape
+    H = h0.shape[1]
+    dx = np.empty((B, T, I), dtype=dtype) if need_dx else None
+    dh0 = np.empty((B, H), dtype=dtype)
+    dw_ih = np.empty((3 * H, I), dtype=dtype)
+    dw_hh = np.empty((3 * H, H), dtype=dtype)
+    db_ih = np.empty((3 * H,), dtype=dtype)
+    db_hh = np.empty((3 * H,), dtype=dtype)
+    rc = getattr(lib, "oracle_gru_backward" + _suffix(dtype))(
+        B, T, I, H, _p(x), _p(h0), _p(w_ih), _p(w_hh), _p(y), _p(cache), _p(dy), _p(dhn),
+        _p(dx), _p(dh0), _p(dw_ih), _p(dw_hh), _p(db_ih), _p(db_hh))
+    if rc != 0:
+        raise MemoryError("oracle_gru_backward failed to allocate")
+    return BackwardResult(dx, dh0, dw_ih, dw_hh, db_ih, db_hh)
+
+
+@dataclass
+class StackResult:
+    y: np.ndarray                 # [B, T, H] output of the last layer
+    hn: np.ndarray                # [L, B, H]
+    dx: np.ndarray                # [B, T, I]
+    dhx: np.ndarray               # [L, B, H]
+    grads: List[dict]             # per layer: weight_ih/weight_hh/bias_ih/bias_hh
+
+
+def stack_forward_backward(x, hx, params: Sequence[dict], dy, dhn=None, dtype=np.float64) -> StackResult:
+    """Multi-layer forward + backward with nn.GRU parameter naming.
+
+    ``params[l]`` holds ``weight_ih``, ``weight_hh``, ``bias_ih``, ``bias_hh``;
+    ``hx`` is [L,B,H] or None (zeros); ``dy`` is the gradient of the last
+    layer's output and ``dhn`` [L,B,H] (or None) the gradient of h_n.
+    """
+    L = len(params)
+    x = np.asarray(x, dtype=dtype)
+    B, T, _ = x.shape
+    H = np.asarray(params[0]["weight_hh"]).shape[1]
+    if hx is None:
+        hx = np.zeros((L, B, H), dtype=dtype)
+    layer_in, fwds, hns = [x], [], []
+    for l in range(L):
+        p = params[l]
+        f = forward(layer_in[-1], hx[l], p["weight_ih"], p["weight_hh"], p["bias_ih"], p["bias_hh"], dtype=dtype)
+        fwds.append(f)
+        hns.append(f.hn)
+        layer_in.append(f.y)
+    grads: List[dict] = [None] * L  # type: ignore[list-item]
+    dhx = np.zeros((L, B, H), dtype=dtype)
+    g_out = np.asarray(dy, dtype=dtype)
+    for l in reversed(range(L)):
+        p = params[l]
+        b = backward(layer_in[l], hx[l], p["weight_ih"], p["weight_hh"], fwds[l].y, fwds[l].cache,
+                     g_out, None if dhn is None else dhn[l], dtype=dtype, need_dx=True)
+        grads[l] = {"weight_ih": b.dw_ih, "weight_hh": b.dw_hh, "bias_ih": b.db_ih, "bias_hh": b.db_hh}
+        dhx[l] = b.dh0
+        g_out = b.dx
+    return StackResult(fwds[-1].y, np.stack(hns, 0), g_out, dhx, grads)

@@ -1,0 +1,108 @@
+"""ctypes binding of librnn_kernel_amd.so (the C ABI in include/rnn_kernel_amd.h).
+
+The reference launches its kernels through cuda-python's driver API with raw
+pointers on torch's current stream (src/rnn_kernel/a100/prod/gru.py:265-300);
+this module is the equivalent thin layer over the HIP library.  There is no
+fallback: if the library is missing or fails to load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "librnn_kernel_amd.so")
+
+# Every exported symbol with (restype, argtypes).
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+SIGNATURES = {
+    "rka_version": (_I, []),
+    "rka_last_error": (ctypes.c_char_p, []),
+    "rka_device_supported": (_I, [_I]),
+    "rka_gru_reserve_bytes": (_SZ, [_I, _I, _I]),
+    "rka_gru_forward_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "rka_gru_forward": (_I, [_P] * 9 + [_P, _SZ, _I, _I, _I, _I, _P]),
+    "rka_gru_backward_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "rka_gru_backward": (_I, [_P] * 14 + [_P, _SZ, _I, _I, _I, _I, _P]),
+    "rka_gemm_f32": (_I, [_I, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _I, _P]),
+    "rka_gru_recurrence_workspace_bytes": (_SZ, [_I, _I]),
+    "rka_gru_recurrence_forward": (_I, [_P] * 7 + [_P, _SZ, _I, _I, _I, _P]),
+    "rka_gru_recurrence_backward": (_I, [_P] * 8 + [_P, _SZ, _I, _I, _I, _P]),
+    "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
+    "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
+    "rka_profile_enable": (_I, [_I]),
+    "rka_profile_read": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
+    "rka_profile_stage_name": (ctypes.c_char_p, [_I]),
+}
+NUM_STAGES = 6
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+
+class RKAError(RuntimeError):
+    """A nonzero status returned by the HIP library."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the library (after torch, so it binds torch's HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        import torch  # noqa: F401  (binds libamdhip64.so.7 to torch's copy first)
+
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"rnn_kernel_amd HIP library not built: {LIB_PATH} is missing. "
+                "Build it with `python -m rnn_kernel_amd.build` (hipcc, gfx950)."
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load().rka_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RKAError(f"{what} failed with status {rc}: {last_error()}")
+
+
+def ptr(t) -> Optional[int]:
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def profile_enable(on: bool) -> None:
+    check(load().rka_profile_enable(1 if on else 0), "rka_profile_enable")
+
+
+def profile_read() -> dict:
+    """{stage name: (total ms, launches)} since the last read; waits for the
+    recorded events."""
+    lib = load()
+    ms = (ctypes.c_double * NUM_STAGES)()
+    cnt = (ctypes.c_int * NUM_STAGES)()
+    check(lib.rka_profile_read(ms, cnt), "rka_profile_read")
+    return {lib.rka_profile_stage_name(i).decode(): (ms[i], cnt[i]) for i in range(NUM_STAGES)}
+
+
+def describe_recurrence(direction: int, batch: int, hidden: int) -> dict:
+    out = (ctypes.c_int * 6)()
+    check(load().rka_describe_recurrence(direction, batch, hidden, out), "rka_describe_recurrence")
+    keys = ("groups", "slices", "units", "rows", "pair_waves", "lds_bytes")
+    return dict(zip(keys, list(out)))

@@ -1,0 +1,308 @@
+// fp32 GEMMs of the GRU path on gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// One kernel template serves the four products of a layer:
+//   input projection  Gx  = X W_ih^T + b_ih        (A row-major, B row-major)
+//   input gradient    dX  = G_i W_ih               (A row-major, B k-major)
+//   weight gradients  dW  = G^T [X | Hprev]        (A k-major,  B k-major)
+// C[m,n] = sum_k A(m,k) B(n,k).  A workgroup of 4 wavefronts computes a
+// 128x128 tile; each wavefront owns a 64x64 quadrant as 2x2 MFMA 32x32
+// blocks.  Operand tiles of 16 k-steps are staged through LDS in k-major form
+// ([k][row], padded) so that the MFMA operand reads of a half-wave are 32
+// consecutive floats (conflict free); the next tile is prefetched into
+// registers while the current one is consumed (double-buffered LDS, one
+// barrier per tile).  The weight gradients (K = B*T rows) use split-K with a
+// fixed-order reduction, so results are deterministic run to run.
+#include "rka_internal.h"
+
+namespace rka {
+namespace {
+
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int BK = 16;
+constexpr int LDSP = BM + 4;  // padded LDS row (floats); multiple of 4 for b128 stores
+constexpr int NT = 256;
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Address of element (row r, k) of an operand; handles the [h0 ; y[:, :-1]]
+// row remap used as the B operand of dW_hh.
+__device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, int k) {
+    if (op.kmajor == 0) return op.ptr + (size_t)r * op.ld + k;
+    if (op.shift_T > 0) {
+        const int t = k % op.shift_T;
+        if (t == 0) return op.shift_first + (size_t)(k / op.shift_T) * op.ld + r;
+        return op.ptr + (size_t)(k - 1) * op.ld + r;
+    }
+    return op.ptr + (size_t)k * op.ld + r;
+}
+
+// Register staging of one BMxBK operand tile (2 float4 per thread).
+// kmajor == 0: thread -> (row tid/4 + 64 i, k 4*(tid%4) .. +3)
+// kmajor == 1: thread -> (k tid/32 + 8 i, row 4*(tid%32) .. +3)
+template <bool VEC>
+__device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int kend,
+                                          int r0, int k0, int tid, float4 (&v)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        int r, k;
+        if (op.kmajor == 0) {
+            r = r0 + tid / 4 + 64 * i;
+            k = k0 + 4 * (tid % 4);
+        } else {
+            k = k0 + tid / 32 + 8 * i;
+            r = r0 + 4 * (tid % 32);
+        }
+        if (VEC) {
+            // Vector path: the contiguous extent is a multiple of 4 and rows
+            // are 16-byte aligned, so a float4 is entirely in or out.
+            const bool in = (r < rows) && (k < kend);
+            v[i] = in ? *reinterpret_cast<const float4*>(elem_ptr(op, r, k))
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            float e[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int rr = op.kmajor == 0 ? r : r + c;
+                const int kk = op.kmajor == 0 ? k + c : k;
+                e[c] = (rr < rows && kk < kend) ? *elem_ptr(op, rr, kk) : 0.f;
+            }
+            v[i] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+    }
+}
+
+__device__ __forceinline__ void store_tile(int kmajor, float* lds, int tid, const float4 (&v)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (kmajor == 0) {
+            const int r = tid / 4 + 64 * i;
+            const int k = 4 * (tid % 4);
+            lds[(k + 0) * LDSP + r] = v[i].x;
+            lds[(k + 1) * LDSP + r] = v[i].y;
+            lds[(k + 2) * LDSP + r] = v[i].z;
+            lds[(k + 3) * LDSP + r] = v[i].w;
+        } else {
+            const int k = tid / 32 + 8 * i;
+            const int r = 4 * (tid % 32);
+            *reinterpret_cast<float4*>(lds + k * LDSP + r) = v[i];
+        }
+    }
+}
+
+struct GemmArgs {
+    GemmOperand a, b;
+    int m, n, k;
+    int kchunk;            // k extent per split (multiple of BK)
+    const float* bias;     // direct mode
+    float* c;              // direct mode output
+    int ldc;
+    float* partial;        // split mode: [ksplit][m][n] then colsum [ksplit][m]
+    int want_colsum;
+};
+
+template <bool AV, bool BV, bool SPLIT>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
+    __shared__ __attribute__((aligned(16))) float As[2][BK * LDSP];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDSP];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int m0 = blockIdx.x * BM;
+    const int n0 = blockIdx.y * BN;
+    const int kbeg = blockIdx.z * p.kchunk;
+    const int kend = min(p.k, kbeg + p.kchunk);
+    const int nkb = (kend - kbeg + BK - 1) / BK;
+    const bool colsum = SPLIT && p.want_colsum && blockIdx.y == 0;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    float cs = 0.f;
+
+    float4 ra[2], rb[2];
+    if (nkb > 0) {
+        load_tile<AV>(p.a, p.m, kend, m0, kbeg, tid, ra);
+        load_tile<BV>(p.b, p.n, kend, n0, kbeg, tid, rb);
+        store_tile(p.a.kmajor, As[0], tid, ra);
+        store_tile(p.b.kmajor, Bs[0], tid, rb);
+    }
+    __syncthreads();
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int cur = kb & 1;
+        const bool more = kb + 1 < nkb;
+        if (more) {
+            load_tile<AV>(p.a, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
+            load_tile<BV>(p.b, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
+        }
+        const float* as = As[cur];
+        const float* bs = Bs[cur];
+        if (colsum && tid < BM) {
+#pragma unroll
+            for (int kk = 0; kk < BK; ++kk) cs += as[kk * LDSP + tid];
+        }
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            const int row = (kk + (lane >> 5)) * LDSP + (lane & 31);
+            const float a0 = as[row + wm * 64];
+            const float a1 = as[row + wm * 64 + 32];
+            const float b0 = bs[row + wn * 64];
+            const float b1 = bs[row + wn * 64 + 32];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (more) {
+            store_tile(p.a.kmajor, As[cur ^ 1], tid, ra);
+            store_tile(p.b.kmajor, Bs[cur ^ 1], tid, rb);
+        }
+        __syncthreads();
+    }
+
+    // Output layout of a 32x32 MFMA block: lane l, register r holds
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n >= p.n) continue;
+            const float bias = (!SPLIT && p.bias) ? p.bias[n] : 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m >= p.m) continue;
+                if (SPLIT) {
+                    p.partial[((size_t)blockIdx.z * p.m + m) * p.n + n] = acc[i][j][r];
+                } else {
+                    p.c[(size_t)m * p.ldc + n] = acc[i][j][r] + bias;
+                }
+            }
+        }
+    }
+    if (colsum && tid < BM && m0 + tid < p.m) {
+        float* cpart = p.partial + (size_t)gridDim.z * p.m * p.n;
+        cpart[(size_t)blockIdx.z * p.m + m0 + tid] = cs;
+    }
+}
+
+// out[o*ldc + n] = sum_z partial[z][(o+rot)%m][n]; colsum likewise.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int ksplit,
+                                                            int m, int n, int rot, float* __restrict__ c,
+                                                            int ldc, float* __restrict__ colsum) {
+    const size_t total = (size_t)m * n + (colsum ? m : 0);
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        if (idx < (size_t)m * n) {
+            const int o = (int)(idx / n);
+            const int col = (int)(idx % n);
+            const int src = rot ? (o + rot) % m : o;
+            float s = 0.f;
+            for (int z = 0; z < ksplit; ++z) s += partial[((size_t)z * m + src) * n + col];
+            c[(size_t)o * ldc + col] = s;
+        } else {
+            const int o = (int)(idx - (size_t)m * n);
+            const int src = rot ? (o + rot) % m : o;
+            const float* cpart = partial + (size_t)ksplit * m * n;
+            float s = 0.f;
+            for (int z = 0; z < ksplit; ++z) s += cpart[(size_t)z * m + src];
+            colsum[o] = s;
+        }
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// A float4 along the contiguous dimension is valid when that dimension's
+// extent and the leading dimension are multiples of 4 and rows are aligned.
+bool vec_ok(const GemmOperand& op, int rows, int k) {
+    const int extent = op.kmajor == 0 ? k : rows;
+    if (extent % 4 != 0 || op.ld % 4 != 0 || !aligned16(op.ptr)) return false;
+    if (op.shift_T > 0 && !aligned16(op.shift_first)) return false;
+    return true;
+}
+
+template <bool SPLIT>
+int launch_gemm(const GemmArgs& args, int ksplit, bool av, bool bv, hipStream_t stream) {
+    dim3 grid((args.m + BM - 1) / BM, (args.n + BN - 1) / BN, ksplit);
+    if (av && bv) {
+        hipLaunchKernelGGL((gemm_f32_kernel<true, true, SPLIT>), grid, dim3(NT), 0, stream, args);
+    } else if (av) {
+        hipLaunchKernelGGL((gemm_f32_kernel<true, false, SPLIT>), grid, dim3(NT), 0, stream, args);
+    } else if (bv) {
+        hipLaunchKernelGGL((gemm_f32_kernel<false, true, SPLIT>), grid, dim3(NT), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL((gemm_f32_kernel<false, false, SPLIT>), grid, dim3(NT), 0, stream, args);
+    }
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace
+
+int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
+                const float* bias, float* c, int ldc, hipStream_t stream) {
+    if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
+    if (!a.ptr || !b.ptr || !c) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: null operand");
+    if (m > 65535 * BM || n > 65535 * BN) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
+    GemmArgs args{};
+    args.a = a;
+    args.b = b;
+    args.m = m;
+    args.n = n;
+    args.k = k;
+    args.kchunk = (k + BK - 1) / BK * BK;
+    args.bias = bias;
+    args.c = c;
+    args.ldc = ldc;
+    return launch_gemm<false>(args, 1, vec_ok(a, m, k), vec_ok(b, n, k), stream);
+}
+
+size_t splitk_partial_floats(int m, int n, int ksplit) {
+    return (size_t)ksplit * m * n + (size_t)ksplit * m;
+}
+
+int choose_ksplit(int m, int n, int k, int num_cus) {
+    const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    const int target = 2 * (num_cus > 0 ? num_cus : 256);
+    int ks = (target + tiles - 1) / tiles;
+    const int max_by_k = k / (8 * BK);  // at least 8 tiles of k per split
+    if (ks > max_by_k) ks = max_by_k;
+    if (ks > 64) ks = 64;
+    if (ks < 1) ks = 1;
+    return ks;
+}
+
+int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
+                float* c, int ldc, float* colsum, int rot,
+                float* partial, int ksplit, hipStream_t stream) {
+    if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
+    if (ksplit < 1) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: ksplit must be >= 1");
+    GemmArgs args{};
+    args.a = a;
+    args.b = b;
+    args.m = m;
+    args.n = n;
+    args.k = k;
+    const int kper = (k + ksplit - 1) / ksplit;
+    args.kchunk = (kper + BK - 1) / BK * BK;
+    args.partial = partial;
+    args.want_colsum = colsum != nullptr;
+    RKA_RETURN_IF_ERR(launch_gemm<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k), stream));
+    const size_t total = (size_t)m * n + (colsum ? m : 0);
+    const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, ksplit, m, n, rot,
+                       c, ldc, colsum);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace rka

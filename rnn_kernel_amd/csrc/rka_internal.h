@@ -1,0 +1,101 @@
+// Internal declarations shared by the rnn_kernel_amd translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/rnn_kernel_amd.h"
+
+namespace rka {
+
+// ---------------------------------------------------------------- errors ---
+void set_error(const std::string& msg);
+void clear_error();
+
+#define RKA_RETURN_IF_HIP(expr)                                                  \
+    do {                                                                         \
+        hipError_t rka_e_ = (expr);                                              \
+        if (rka_e_ != hipSuccess) {                                              \
+            ::rka::set_error(std::string(#expr) + ": " + hipGetErrorString(rka_e_)); \
+            return static_cast<int>(rka_e_);                                     \
+        }                                                                        \
+    } while (0)
+
+#define RKA_RETURN_IF_ERR(expr)      \
+    do {                             \
+        int rka_rc_ = (expr);        \
+        if (rka_rc_ != 0) return rka_rc_; \
+    } while (0)
+
+int fail(int code, const std::string& msg);
+
+// ------------------------------------------------------- device queries ---
+struct DeviceInfo {
+    int device = -1;
+    int num_cus = 0;
+    int max_lds_per_block = 0;
+    bool gfx950 = false;
+    bool cooperative = false;
+    std::string arch;
+};
+// Cached per device; returns 0 or an error code.
+int current_device_info(const DeviceInfo** out);
+
+// --------------------------------------------------------------- layout ---
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ----------------------------------------------------------------- GEMM ---
+struct GemmOperand {
+    const float* ptr = nullptr;
+    int ld = 0;
+    int kmajor = 0;            // 0: element (r,k) at ptr[r*ld+k]; 1: at ptr[k*ld+r]
+    // Row remap for k-major operands used by the dW_hh product: when
+    // shift_T > 0, k = b*shift_T + t reads row k-1 of ptr for t > 0 and row b
+    // of shift_first (ld shift_ld) for t == 0, i.e. the rows of
+    // [h0 ; y[:, :-1]] without materialising them.
+    int shift_T = 0;
+    const float* shift_first = nullptr;
+};
+
+// C[m,n] = sum_k A(m,k) B(n,k) + bias[n]; direct store.
+int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
+                const float* bias, float* c, int ldc, hipStream_t stream);
+
+// Split-K product with deterministic reduction.  Output rows are rotated:
+// out[o] = C[(o + rot) % m] (rot = 0: no rotation).  colsum (nullable)
+// receives sum_k A(m,k) with the same rotation.  partial must hold
+// splitk_partial_floats(m, n, ksplit) floats.
+int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
+                float* c, int ldc, float* colsum, int rot,
+                float* partial, int ksplit, hipStream_t stream);
+size_t splitk_partial_floats(int m, int n, int ksplit);
+int choose_ksplit(int m, int n, int k, int num_cus);
+
+// ----------------------------------------------------------- recurrence ---
+struct RecConfig {
+    int groups = 0;        // batch-row groups
+    int slices = 0;        // hidden-unit slices
+    int units = 0;         // hidden units per slice (divides 64)
+    int rows = 0;          // batch rows per group
+    int pair_waves = 0;    // wavefronts holding (row, unit) pairs
+    int lds_bytes = 0;
+};
+int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, RecConfig* cfg);
+
+size_t rec_workspace_bytes(int batch, int hidden);
+
+int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
+                       float* y, float* hn, float* reserve, void* ws, size_t ws_bytes,
+                       int B, int T, int H, hipStream_t stream);
+int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,
+                        const float* h0, const float* y, const float* w_hh,
+                        float* g, float* dh0, void* ws, size_t ws_bytes,
+                        int B, int T, int H, hipStream_t stream);
+
+extern int g_override_units[2];
+extern int g_override_pair_waves[2];
+
+}  // namespace rka

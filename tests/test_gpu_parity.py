@@ -1,0 +1,366 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle and with
+torch.nn.GRU fp32 on the same GPU.
+
+Tolerances (stated by the north star): outputs and h_n within max-abs 1e-4;
+gradients within max|g - g_ref| / max|g_ref| <= 1e-3 per tensor.  Small shapes
+are checked against the float64 oracle; the BASELINE configurations are
+checked against torch.nn.GRU fp32 (TF32 off) on the same GPU and, for a
+subset of batch rows, against the float64 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+OUT_ATOL = 1e-4
+GRAD_REL = 1e-3
+
+
+def _rel(a, b):
+    a = a.detach().double().cpu()
+    b = torch.as_tensor(b).double().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def _maxabs(a, b):
+    return float((a.detach().double().cpu() - torch.as_tensor(b).double().cpu()).abs().max())
+
+
+def _no_tf32():
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+
+
+# ------------------------------------------------------------------ GEMM ---
+GEMM_SHAPES = [(128, 128, 16), (300, 200, 50), (1, 1, 1), (4096, 768, 256), (129, 387, 130), (768, 256, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+@pytest.mark.parametrize("a_kmajor,b_kmajor", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_matches_float64(gpu, hip_lib, m, n, k, a_kmajor, b_kmajor):
+    from rnn_kernel_amd import _lib
+
+    print(f"gemm m={m} n={n} k={k} a_kmajor={a_kmajor} b_kmajor={b_kmajor}", flush=True)
+    g = torch.Generator().manual_seed(m * 7 + n * 3 + k)
+    A = torch.randn(m, k, generator=g)
+    Bm = torch.randn(n, k, generator=g)
+    bias = torch.randn(n, generator=g)
+    ref = A.double() @ Bm.double().T + bias.double()
+    a_store = (A.T if a_kmajor else A).contiguous().to(gpu)
+    b_store = (Bm.T if b_kmajor else Bm).contiguous().to(gpu)
+    lda = m if a_kmajor else k
+    ldb = n if b_kmajor else k
+    c = torch.full((m, n), float("nan"), device=gpu)
+    rc = hip_lib.rka_gemm_f32(m, n, k, a_store.data_ptr(), lda, a_kmajor, b_store.data_ptr(), ldb, b_kmajor,
+                              bias.to(gpu).data_ptr(), c.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "rka_gemm_f32")
+    torch.cuda.synchronize()
+    err = (c.double().cpu() - ref).abs().max().item()
+    assert err <= 1e-6 * k + 1e-5, err
+
+
+def test_gemm_unaligned_operands_use_scalar_path(gpu, hip_lib):
+    """Operands offset by one float (not 16-byte aligned) and odd leading dims."""
+    from rnn_kernel_amd import _lib
+
+    m, n, k = 77, 45, 33
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn(m, k + 3, generator=g)
+    Bm = torch.randn(n, k + 3, generator=g)
+    ref = A[:, 1:k + 1].double() @ Bm[:, 1:k + 1].double().T
+    ad, bd = A.to(gpu), Bm.to(gpu)
+    c = torch.empty(m, n + 2, device=gpu)
+    rc = hip_lib.rka_gemm_f32(m, n, k, ad.data_ptr() + 4, k + 3, 0, bd.data_ptr() + 4, k + 3, 0, None,
+                              c.data_ptr(), n + 2, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "rka_gemm_f32")
+    torch.cuda.synchronize()
+    assert (c[:, :n].double().cpu() - ref).abs().max().item() < 1e-4
+
+
+# ------------------------------------------- single layer vs the oracle ---
+LAYER_SHAPES = [
+    # B, T, I, H
+    (2, 8, 16, 16),
+    (3, 5, 4, 129),      # odd H tails
+    (2, 7, 3, 130),
+    (64, 16, 256, 256),  # BASELINE config 2 width, short T
+    (5, 3, 2, 1),        # H = 1
+    (1, 1, 1, 64),       # single step, single row
+    (9, 6, 5, 96),       # batch not a multiple of the row group
+]
+
+
+def _layer_inputs(B, T, I, H, seed, h0_scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    k = 1.0 / H ** 0.5
+    p = {
+        "weight_ih": (torch.rand(3 * H, I, generator=g) * 2 - 1) * k,
+        "weight_hh": (torch.rand(3 * H, H, generator=g) * 2 - 1) * k,
+        "bias_ih": (torch.rand(3 * H, generator=g) * 2 - 1) * k,
+        "bias_hh": (torch.rand(3 * H, generator=g) * 2 - 1) * k,
+    }
+    x = torch.randn(B, T, I, generator=g)
+    h0 = h0_scale * torch.randn(B, H, generator=g)
+    dy = torch.randn(B, T, H, generator=g)
+    dhn = torch.randn(B, H, generator=g)
+    return p, x, h0, dy, dhn
+
+
+@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES)
+def test_layer_forward_backward_matches_oracle(gpu, oracle, B, T, I, H):
+    from rnn_kernel_amd import GRUFunction
+
+    print(f"layer vs oracle B={B} T={T} I={I} H={H}", flush=True)
+    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B * 1000 + T * 10 + H)
+    f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
+                       p["bias_ih"].numpy(), p["bias_hh"].numpy())
+    ref = oracle.backward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(), f.y, f.cache,
+                          dy.numpy(), dhn.numpy())
+    xd = x.to(gpu).requires_grad_(True)
+    h0d = h0.to(gpu).requires_grad_(True)
+    pd = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
+    y, hn = GRUFunction.apply(xd, h0d, pd["weight_ih"], pd["weight_hh"], pd["bias_ih"], pd["bias_hh"])
+    torch.autograd.backward([y, hn], [dy.to(gpu), dhn.to(gpu)[None]])
+    torch.cuda.synchronize()
+    assert _maxabs(y, f.y) <= OUT_ATOL
+    assert _maxabs(hn[0], f.hn) <= OUT_ATOL
+    assert _rel(xd.grad, ref.dx) <= GRAD_REL
+    assert _rel(h0d.grad, ref.dh0) <= GRAD_REL
+    assert _rel(pd["weight_ih"].grad, ref.dw_ih) <= GRAD_REL
+    assert _rel(pd["weight_hh"].grad, ref.dw_hh) <= GRAD_REL
+    assert _rel(pd["bias_ih"].grad, ref.db_ih) <= GRAD_REL
+    assert _rel(pd["bias_hh"].grad, ref.db_hh) <= GRAD_REL
+
+
+def test_recurrence_reserve_layout_matches_oracle_cache(gpu, oracle, hip_lib):
+    """The forward recurrence's reserve is (r, z, n, a_n) per [b, t] row."""
+    from rnn_kernel_amd import _lib
+
+    B, T, I, H = 4, 6, 8, 40
+    p, x, h0, _, _ = _layer_inputs(B, T, I, H, seed=77)
+    f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
+                       p["bias_ih"].numpy(), p["bias_hh"].numpy())
+    gx = (x.double() @ p["weight_ih"].double().T + p["bias_ih"].double()).float().contiguous().to(gpu)
+    y = torch.empty(B, T, H, device=gpu)
+    hn = torch.empty(B, H, device=gpu)
+    res = torch.empty(B, T, 4 * H, device=gpu)
+    ws_bytes = hip_lib.rka_gru_recurrence_workspace_bytes(B, H)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
+    whh, bhh, h0d = (t.contiguous().to(gpu) for t in (p["weight_hh"], p["bias_hh"], h0))
+    rc = hip_lib.rka_gru_recurrence_forward(gx.data_ptr(), h0d.data_ptr(), whh.data_ptr(), bhh.data_ptr(),
+                                            y.data_ptr(), hn.data_ptr(), res.data_ptr(), ws.data_ptr(), ws_bytes,
+                                            B, T, H, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "rka_gru_recurrence_forward")
+    torch.cuda.synchronize()
+    assert _maxabs(res, f.cache) <= 1e-5
+    assert _maxabs(y, f.y) <= 1e-5
+
+
+# ----------------------------------- module vs torch.nn.GRU on the GPU ---
+@pytest.mark.parametrize("input_size", [1, 16])
+@pytest.mark.parametrize("num_layers", [1, 2, 3, 4])
+def test_from_torch_gru_matches_torch_gru(gpu, num_layers, input_size):
+    """Mirror of the reference's prod parity test (tests/test_a100_prod.py:84-126)
+    with the same shapes and tolerances."""
+    from rnn_kernel_amd import from_torch_gru
+
+    _no_tf32()
+    torch.manual_seed(2130 + num_layers * 10 + input_size)
+    hidden, batch, seq = 256, 2, 5
+    torch_gru = torch.nn.GRU(input_size, hidden, num_layers=num_layers, batch_first=True).to(gpu)
+    ours = from_torch_gru(torch_gru)
+    x_t = torch.randn(batch, seq, input_size, device=gpu, requires_grad=True)
+    x_o = x_t.detach().clone().requires_grad_(True)
+    h_t = torch.randn(num_layers, batch, hidden, device=gpu, requires_grad=True)
+    h_o = h_t.detach().clone().requires_grad_(True)
+    out_t, hn_t = torch_gru(x_t, h_t)
+    out_o, hn_o = ours(x_o, h_o)
+    g_out = torch.randn_like(out_t)
+    g_h = torch.randn_like(hn_t)
+    out_t.backward(g_out, retain_graph=True)
+    hn_t.backward(g_h)
+    out_o.backward(g_out, retain_graph=True)
+    hn_o.backward(g_h)
+    assert torch.allclose(out_t, out_o, atol=4e-4, rtol=1e-4)
+    assert torch.allclose(hn_t, hn_o, atol=4e-4, rtol=1e-4)
+    assert torch.allclose(x_t.grad, x_o.grad, atol=1e-3, rtol=3e-4)
+    assert torch.allclose(h_t.grad, h_o.grad, atol=1e-3, rtol=3e-4)
+    for name, p in torch_gru.named_parameters():
+        assert torch.allclose(p.grad, getattr(ours, name).grad, atol=5e-3, rtol=1e-3), name
+
+
+@pytest.mark.parametrize("num_layers", [1, 3])
+def test_inference_paths_match_torch_gru(gpu, num_layers):
+    """no_grad and forward_inference take the cache-free path
+    (reference tests/test_a100_prod.py:129-162)."""
+    from rnn_kernel_amd import from_torch_gru
+
+    _no_tf32()
+    torch.manual_seed(2133 + num_layers)
+    torch_gru = torch.nn.GRU(16, 256, num_layers=num_layers, batch_first=True).to(gpu)
+    ours = from_torch_gru(torch_gru)
+    x = torch.randn(2, 5, 16, device=gpu)
+    h0 = torch.randn(num_layers, 2, 256, device=gpu)
+    with torch.no_grad():
+        out_t, hn_t = torch_gru(x, h0)
+        out_n, hn_n = ours(x, h0)
+    out_e, hn_e = ours.forward_inference(x, h0)
+    assert not out_n.requires_grad and not out_e.requires_grad
+    for a, b in ((out_t, out_n), (hn_t, hn_n), (out_t, out_e), (hn_t, hn_e)):
+        assert torch.allclose(a, b, atol=4e-4, rtol=1e-4)
+
+
+def test_loss_on_final_hidden_only_and_output_only(gpu):
+    """grad_output None (loss on h_n only) and grad_h_n None (loss on output only)."""
+    from rnn_kernel_amd import from_torch_gru
+
+    _no_tf32()
+    torch.manual_seed(414)
+    torch_gru = torch.nn.GRU(8, 64, batch_first=True).to(gpu)
+    ours = from_torch_gru(torch_gru)
+    x = torch.randn(3, 7, 8, device=gpu)
+    for which in ("hn", "out"):
+        torch_gru.zero_grad()
+        ours.zero_grad()
+        out_t, hn_t = torch_gru(x)
+        out_o, hn_o = ours(x)
+        (hn_t.square().sum() if which == "hn" else out_t.square().sum()).backward()
+        (hn_o.square().sum() if which == "hn" else out_o.square().sum()).backward()
+        for name, p in torch_gru.named_parameters():
+            assert _rel(getattr(ours, name).grad, p.grad) <= GRAD_REL, (which, name)
+
+
+def test_repeat_runs_are_bitwise_identical(gpu):
+    from rnn_kernel_amd import GRU
+
+    torch.manual_seed(99)
+    model = GRU(32, 128).to(gpu)
+    x = torch.randn(16, 40, 32, device=gpu)
+    results = []
+    for _ in range(2):
+        model.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        y, hn = model(xi)
+        (y.sin().sum() + hn.sum()).backward()
+        results.append([y.detach().clone(), hn.detach().clone(), xi.grad.clone()] +
+                       [p.grad.clone() for p in model.parameters()])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fwd_units,bwd_units", [(1, 1), (4, 16), (64, 2)])
+def test_alternative_decompositions_agree(gpu, hip_lib, fwd_units, bwd_units):
+    """Other (units, pair-wave) tilings of the recurrences give the same answer."""
+    from rnn_kernel_amd import GRU
+
+    torch.manual_seed(5)
+    model = GRU(24, 72).to(gpu)
+    x = torch.randn(10, 9, 24, device=gpu)
+
+    def run():
+        model.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        y, hn = model(xi)
+        (y.cos().sum() + hn.sum()).backward()
+        return [y.detach().clone(), xi.grad.clone()] + [p.grad.clone() for p in model.parameters()]
+
+    base = run()
+    assert hip_lib.rka_set_recurrence_config(fwd_units, 0, bwd_units, 0) == 0
+    try:
+        alt = run()
+    finally:
+        hip_lib.rka_set_recurrence_config(0, 0, 0, 0)
+    for a, b in zip(base, alt):
+        assert _rel(a, b) <= 1e-5
+
+
+# ------------------------------------------------- BASELINE configurations ---
+def _torch_reference(gpu, L, I, H, B, T, seed, h0_scale, x_hook=None, chunks=1):
+    """Our model and torch.nn.GRU with identical weights/inputs; MSE loss vs
+    N(0,1) target.  Returns (ours, theirs) dicts of results."""
+    from rnn_kernel_amd import from_torch_gru
+
+    _no_tf32()
+    torch.manual_seed(seed)
+    torch_gru = torch.nn.GRU(I, H, num_layers=L, batch_first=True)
+    x = torch.randn(B, T, I)
+    if x_hook is not None:
+        x = x_hook(x)
+    h0 = h0_scale * torch.randn(L, B, H)
+    target = torch.randn(B, T, H)
+    torch_gru = torch_gru.to(gpu)
+    ours = from_torch_gru(torch_gru)
+    res = {}
+    for name, model in (("ours", ours), ("torch", torch_gru)):
+        xi = x.to(gpu).requires_grad_(True)
+        hi = h0.to(gpu).requires_grad_(True)
+        if chunks == 1:
+            out, hn = model(xi, hi)
+        else:
+            outs, hidden = [], hi
+            for c in xi.chunk(chunks, dim=1):
+                o, hidden = model(c, hidden)
+                outs.append(o)
+            out, hn = torch.cat(outs, dim=1), hidden
+        loss = torch.nn.functional.mse_loss(out, target.to(gpu))
+        loss.backward()
+        res[name] = {"out": out.detach(), "hn": hn.detach(), "dx": xi.grad, "dh0": hi.grad,
+                     **{n: p.grad for n, p in model.named_parameters()}}
+    return res, (torch_gru, x, h0, target)
+
+
+def _assert_parity(res, label):
+    o, t = res["ours"], res["torch"]
+    assert _maxabs(o["out"], t["out"]) <= OUT_ATOL, label
+    assert _maxabs(o["hn"], t["hn"]) <= OUT_ATOL, label
+    for k in o:
+        if k in ("out", "hn"):
+            continue
+        assert _rel(o[k], t[k]) <= GRAD_REL, (label, k, _rel(o[k], t[k]))
+
+
+def test_config2_north_star_matches_torch_gru_and_oracle_rows(gpu, oracle):
+    """I=256, H=256, B=64, T=512, h0 ~ 0.1 N(0,1), MSE loss."""
+    print("config2 B=64 T=512 I=256 H=256", flush=True)
+    res, (torch_gru, x, h0, target) = _torch_reference(gpu, 1, 256, 256, 64, 512, seed=42, h0_scale=0.1)
+    _assert_parity(res, "c2")
+    # Rows 0 and 1 against the float64 oracle: y and dx depend only on their own row.
+    p = {n: getattr(torch_gru, f"{n}_l0").detach().cpu().numpy()
+         for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")}
+    rows = slice(0, 2)
+    f = oracle.forward(x[rows].numpy(), h0[0, rows].numpy(), p["weight_ih"], p["weight_hh"], p["bias_ih"],
+                       p["bias_hh"])
+    dy = (2.0 / target.numel()) * (res["ours"]["out"][rows].cpu().double().numpy() - target[rows].numpy())
+    b = oracle.backward(x[rows].numpy(), h0[0, rows].numpy(), p["weight_ih"], p["weight_hh"], f.y, f.cache,
+                        dy, None)
+    assert _maxabs(res["ours"]["out"][rows], f.y) <= OUT_ATOL
+    assert _rel(res["ours"]["dx"][rows], b.dx) <= GRAD_REL
+    assert _rel(res["ours"]["dh0"][0, rows], b.dh0) <= GRAD_REL
+
+
+@pytest.mark.parametrize("H", [64, 96, 128, 129, 130, 160, 192])
+def test_config3_hidden_sweep_matches_torch_gru(gpu, H):
+    print(f"config3 H={H}", flush=True)
+    res, _ = _torch_reference(gpu, 1, H, H, 64, 512, seed=42 + H, h0_scale=0.1)
+    _assert_parity(res, f"c3 H={H}")
+
+
+def test_config4_stacked_two_layers_matches_torch_gru(gpu):
+    print("config4 L=2 B=256 T=1024 H=256", flush=True)
+    res, _ = _torch_reference(gpu, 2, 256, 256, 256, 1024, seed=44, h0_scale=0.0)
+    _assert_parity(res, "c4")
+
+
+def test_config5_chunked_bptt_matches_full_sequence(gpu):
+    """I=128, H=256, B=16, T=4096 as 8 chunks of 512 carrying h (no detach),
+    h0 ~ 0.5 N(0,1), 5% of [B,T] rows of x scaled x10."""
+    print("config5 chunked", flush=True)
+
+    def saturate(x):
+        g = torch.Generator().manual_seed(4242)
+        mask = torch.rand(x.shape[0], x.shape[1], generator=g) < 0.05
+        return torch.where(mask[..., None], x * 10.0, x)
+
+    res, _ = _torch_reference(gpu, 1, 128, 256, 16, 4096, seed=45, h0_scale=0.5, x_hook=saturate, chunks=8)
+    _assert_parity(res, "c5")
