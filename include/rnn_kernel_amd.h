@@ -136,17 +136,24 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
                                 int batch, int seq_len, int hidden_size,
                                 void* stream);
 
-/* Override the recurrence work decomposition (0 = automatic choice).
- * units: hidden units per workgroup (a divisor of 64);
- * pair_waves: wavefronts holding (row, unit) pairs (1, 2 or 4).
- * Affects later calls on all threads.  For tuning and tests. */
-int rka_set_recurrence_config(int fwd_units, int fwd_pair_waves,
-                              int bwd_units, int bwd_pair_waves);
+/* Override the recurrence kernel choice for direction `dir` (0 forward,
+ * 1 backward); affects later calls on all threads.  For tuning and tests.
+ * kind 0: automatic (register-resident kernel when hidden_size <= 256 and it
+ *         fits resident, else LDS-tiled);
+ * kind 1: LDS-tiled; units = hidden units per workgroup (a divisor of 64,
+ *         0 = auto), param = wavefronts holding (row, unit) pairs (1, 2, 4,
+ *         0 = auto);
+ * kind 2: register-resident; units ignored, param = batch rows per
+ *         workgroup (1, 2, 4, 0 = auto). */
+#define RKA_REC_AUTO 0
+#define RKA_REC_TILED 1
+#define RKA_REC_REGISTER 2
+int rka_set_recurrence_config(int dir, int kind, int units, int param);
 
 /* Describe the decomposition the next recurrence call would use for this
- * shape: writes {groups, slices, units, rows_per_group, pair_waves,
- * lds_bytes} for the forward (dir=0) or backward (dir=1) kernel. */
-int rka_describe_recurrence(int dir, int batch, int hidden_size, int out6[6]);
+ * shape: writes {kind, groups, slices, units, rows_per_group, pair_waves,
+ * chunk, lds_bytes}. */
+int rka_describe_recurrence(int dir, int batch, int hidden_size, int out8[8]);
 
 
 /*

@@ -101,8 +101,18 @@ def profile_read() -> dict:
     return {lib.rka_profile_stage_name(i).decode(): (ms[i], cnt[i]) for i in range(NUM_STAGES)}
 
 
+REC_KINDS = {0: "auto", 1: "tiled", 2: "register"}
+
+
 def describe_recurrence(direction: int, batch: int, hidden: int) -> dict:
-    out = (ctypes.c_int * 6)()
+    """Decomposition the next recurrence call would use (0 forward, 1 backward)."""
+    out = (ctypes.c_int * 8)()
     check(load().rka_describe_recurrence(direction, batch, hidden, out), "rka_describe_recurrence")
-    keys = ("groups", "slices", "units", "rows", "pair_waves", "lds_bytes")
-    return dict(zip(keys, list(out)))
+    keys = ("kind", "groups", "slices", "units", "rows", "pair_waves", "chunk", "lds_bytes")
+    d = dict(zip(keys, list(out)))
+    d["kind"] = REC_KINDS.get(d["kind"], d["kind"])
+    return d
+
+
+def set_recurrence_config(direction: int, kind: int = 0, units: int = 0, param: int = 0) -> None:
+    check(load().rka_set_recurrence_config(direction, kind, units, param), "rka_set_recurrence_config")

@@ -1,0 +1,423 @@
+// Register-resident persistent GRU recurrences (hidden size <= 256).
+//
+// Workgroup (g, s) owns hidden units [64 s, 64 s + 64) of batch rows
+// [ROWS g, ROWS g + ROWS); lane l of every wavefront is unit 64 s + l.  The
+// W_hh entries the workgroup needs live in VGPRs for the whole sequence:
+//   forward : wavefront w holds, per lane, the k-chunk [w*chunk, (w+1)*chunk)
+//             of the three rows (r, z, n) of its unit (3*chunk registers);
+//   backward: wavefront w holds, per lane, the j-chunk of its unit's column
+//             of W_hh over the 3H gate rows (chunk registers).
+// Each step a wavefront polls only the exchanged words of its own chunk
+// (h_{t-1} forward, G_h,t backward; one word per lane), broadcasts them with
+// readlane into scalar operands and runs the chunk's FMAs without touching
+// LDS; the 8 wavefront partials are reduced in LDS (one barrier per step) and
+// wavefront r applies the gate math of row r.  With 64 units per workgroup a
+// hidden size of 256 needs 4 exchanging workgroups per batch row.
+//
+// Forward maths (src/rnn_kernel/a100/prod/kernels/a100_gru_h256_kernels.cu:756-776):
+//   a = W_hh h_{t-1} + b_hh; r = sigmoid(gx_r + a_r); z = sigmoid(gx_z + a_z);
+//   n = tanh(gx_n + r a_n); h_t = n + z (h_{t-1} - n); reserve = (r, z, n, a_n)
+// Backward maths (a100_gru_h256_kernels.cu:842-866,915-932), g = dh_t + dy_t:
+//   dz = g (h_{t-1} - n), dn^ = g (1 - z)(1 - n^2), dr^ = dn^ a_n r (1 - r),
+//   dz^ = dz z (1 - z), da_n = dn^ r; dh_{t-1} = g z + G_h W_hh;
+//   g_out[b,t] = (da_n, dr^, dz^, dn^).
+#include "rec_common.h"
+
+#include <algorithm>
+
+namespace rka {
+namespace {
+
+using rec::NTH;
+using rec::NW;
+
+struct RegParams {
+    int B, T, H;
+    int G, S;      // groups of ROWS rows, slices of 64 units
+    int chunk;     // k (forward) or j (backward) values per wavefront
+    int wvec;      // forward: W_hh rows may be read as aligned float4
+};
+
+// ------------------------------------------------------------- forward ---
+template <int NK, int ROWS>
+__global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
+    const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
+    const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
+    float* __restrict__ reserve, unsigned long long* __restrict__ exch, int* __restrict__ abort_flag,
+    RegParams p) {
+    __shared__ float part[2][NW][3][ROWS][64];
+    __shared__ int s_abort;
+
+    const int B = p.B, T = p.T, H = p.H;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = blockIdx.x % p.G;
+    const int s = blockIdx.x / p.G;
+    const int u = s * 64 + lane;
+    const bool uvalid = u < H;
+    const int row0 = g * ROWS;
+    const int kbeg = wave * p.chunk;
+
+    // k-chunk of the three W_hh rows of unit u
+    float wr[NK], wz[NK], wn[NK];
+    const bool vec = p.wvec != 0;
+#pragma unroll
+    for (int k = 0; k < NK; k += 4) {
+        const int kk = kbeg + k;
+        const float* pr = w_hh + (size_t)u * H + kk;
+        const float* pz = pr + (size_t)H * H;
+        const float* pn = pz + (size_t)H * H;
+        if (vec) {
+            const bool ok = uvalid && k < p.chunk && kk < H;
+            const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 a = ok ? *reinterpret_cast<const float4*>(pr) : z4;
+            const float4 b = ok ? *reinterpret_cast<const float4*>(pz) : z4;
+            const float4 c = ok ? *reinterpret_cast<const float4*>(pn) : z4;
+            wr[k] = a.x; wr[k + 1] = a.y; wr[k + 2] = a.z; wr[k + 3] = a.w;
+            wz[k] = b.x; wz[k + 1] = b.y; wz[k + 2] = b.z; wz[k + 3] = b.w;
+            wn[k] = c.x; wn[k + 1] = c.y; wn[k + 2] = c.z; wn[k + 3] = c.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const bool ok = uvalid && k + c < p.chunk && kk + c < H;
+                wr[k + c] = ok ? pr[c] : 0.f;
+                wz[k + c] = ok ? pz[c] : 0.f;
+                wn[k + c] = ok ? pn[c] : 0.f;
+            }
+        }
+    }
+
+    // gate math state of wavefront r < ROWS: row row0 + wave, unit u
+    const int prow = row0 + wave;
+    const bool owner = wave < ROWS && prow < B && uvalid;
+    float h_prev = 0.f, bias_r = 0.f, bias_z = 0.f, bias_n = 0.f, gxr = 0.f, gxz = 0.f, gxn = 0.f;
+    if (owner) {
+        h_prev = h0[(size_t)prow * H + u];
+        bias_r = b_hh[u];
+        bias_z = b_hh[H + u];
+        bias_n = b_hh[2 * H + u];
+        const float* gp = gx + (size_t)prow * T * 3 * H;
+        gxr = gp[u];
+        gxz = gp[H + u];
+        gxn = gp[2 * H + u];
+    }
+    if (threadIdx.x == 0) s_abort = 0;
+    __syncthreads();
+
+    const int kk = kbeg + lane;
+    const bool kvalid = lane < p.chunk && kk < H;
+    bool aborted = false;
+    for (int t = 0; t < T; ++t) {
+        // h_{t-1}[row][kbeg + lane]
+        float hv[ROWS];
+        if (t == 0) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+                hv[r] = (kvalid && row0 + r < B) ? h0[(size_t)(row0 + r) * H + kk] : 0.f;
+        } else {
+            const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H;
+            unsigned long long w[ROWS];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+                w[r] = (kvalid && row0 + r < B) ? rec::load_word(src + (size_t)(row0 + r) * H + kk) : 0ull;
+            bool ok = true;
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                hv[r] = (kvalid && row0 + r < B)
+                            ? rec::wait_word(src + (size_t)(row0 + r) * H + kk, w[r], (unsigned)t, abort_flag, ok)
+                            : 0.f;
+            }
+            if (!ok) s_abort = 1;
+        }
+        float ar[ROWS], az[ROWS], an[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) ar[r] = az[r] = an[r] = 0.f;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const float hk = rec::bcast(hv[r], k);
+                ar[r] = fmaf(hk, wr[k], ar[r]);
+                az[r] = fmaf(hk, wz[k], az[r]);
+                an[r] = fmaf(hk, wn[k], an[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            part[t & 1][wave][0][r][lane] = ar[r];
+            part[t & 1][wave][1][r][lane] = az[r];
+            part[t & 1][wave][2][r][lane] = an[r];
+        }
+        __syncthreads();
+        if (s_abort) {
+            aborted = true;
+            break;
+        }
+        if (owner) {
+            float sr = bias_r, sz = bias_z, sn = bias_n;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) {
+                sr += part[t & 1][w2][0][wave][lane];
+                sz += part[t & 1][w2][1][wave][lane];
+                sn += part[t & 1][w2][2][wave][lane];
+            }
+            const float r = rec::sigmoid_f(gxr + sr);
+            const float z = rec::sigmoid_f(gxz + sz);
+            const float n = tanhf(gxn + r * sn);
+            const float h = n + z * (h_prev - n);
+            rec::store_word(exch + (size_t)(t & 1) * B * H + (size_t)prow * H + u, rec::pack_word(h, (unsigned)(t + 1)));
+            const size_t bt = (size_t)prow * T + t;
+            y[bt * H + u] = h;
+            if (reserve) {
+                float* cp = reserve + bt * 4 * H;
+                cp[u] = r;
+                cp[H + u] = z;
+                cp[2 * H + u] = n;
+                cp[3 * H + u] = sn;
+            }
+            h_prev = h;
+            if (t + 1 < T) {
+                const float* gp = gx + (bt + 1) * 3 * H;
+                gxr = gp[u];
+                gxz = gp[H + u];
+                gxn = gp[2 * H + u];
+            }
+        }
+    }
+    if (owner) hn[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : h_prev;
+}
+
+// ------------------------------------------------------------ backward ---
+template <int NJ, int ROWS>
+__global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
+    const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
+    const float* __restrict__ h0, const float* __restrict__ y, const float* __restrict__ w_hh,
+    float* __restrict__ gout, float* __restrict__ dh0, unsigned long long* __restrict__ exch,
+    int* __restrict__ abort_flag, RegParams p) {
+    __shared__ float part[2][NW][ROWS][64];
+    __shared__ int s_abort;
+
+    const int B = p.B, T = p.T, H = p.H;
+    const int H3 = 3 * H;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = blockIdx.x % p.G;
+    const int s = blockIdx.x / p.G;
+    const int u = s * 64 + lane;
+    const bool uvalid = u < H;
+    const int row0 = g * ROWS;
+    const int jbeg = wave * p.chunk;
+
+    // j-chunk of column u of W_hh (coalesced: lanes read consecutive units)
+    float w[NJ];
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+        const int j = jbeg + jj;
+        w[jj] = (uvalid && jj < p.chunk && j < H3) ? w_hh[(size_t)j * H + u] : 0.f;
+    }
+
+    const int prow = row0 + wave;
+    const bool owner = wave < ROWS && prow < B && uvalid;
+    float dh = 0.f, dyv = 0.f, cr = 0.f, cz = 0.f, cn = 0.f, ca = 0.f, hp = 0.f;
+    if (owner) {
+        if (dhn) dh = dhn[(size_t)prow * H + u];
+        const size_t bt = (size_t)prow * T + (T - 1);
+        if (dy) dyv = dy[bt * H + u];
+        const float* cp = reserve + bt * 4 * H;
+        cr = cp[u];
+        cz = cp[H + u];
+        cn = cp[2 * H + u];
+        ca = cp[3 * H + u];
+        hp = (T > 1) ? y[(bt - 1) * H + u] : h0[(size_t)prow * H + u];
+    }
+    if (threadIdx.x == 0) s_abort = 0;
+    __syncthreads();
+
+    const int j0 = jbeg + lane;
+    const int j1 = jbeg + 64 + lane;
+    const bool v0 = lane < p.chunk && j0 < H3;
+    const bool v1 = NJ > 64 && 64 + lane < p.chunk && j1 < H3;
+    bool aborted = false;
+    float ddirect = 0.f;
+    for (int i = 0; i < T; ++i) {
+        const int t = T - 1 - i;
+        unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
+        const unsigned tag = (unsigned)(i + 1);
+        if (owner) {
+            const float gsum = dh + dyv;
+            const float dz = gsum * (hp - cn);
+            const float dnh = gsum * (1.0f - cz) * (1.0f - cn * cn);
+            const float dan = dnh * cr;
+            const float drh = dnh * ca * cr * (1.0f - cr);
+            const float dzh = dz * cz * (1.0f - cz);
+            ddirect = gsum * cz;
+            unsigned long long* wp = slotp + (size_t)prow * H3 + u;
+            rec::store_word(wp, rec::pack_word(drh, tag));
+            rec::store_word(wp + H, rec::pack_word(dzh, tag));
+            rec::store_word(wp + 2 * H, rec::pack_word(dan, tag));
+            const size_t bt = (size_t)prow * T + t;
+            float* op = gout + bt * 4 * H;
+            op[u] = dan;
+            op[H + u] = drh;
+            op[2 * H + u] = dzh;
+            op[3 * H + u] = dnh;
+            if (t > 0) {
+                const size_t pbt = bt - 1;
+                dyv = dy ? dy[pbt * H + u] : 0.f;
+                const float* cp = reserve + pbt * 4 * H;
+                cr = cp[u];
+                cz = cp[H + u];
+                cn = cp[2 * H + u];
+                ca = cp[3 * H + u];
+                hp = (t > 1) ? y[(pbt - 1) * H + u] : h0[(size_t)prow * H + u];
+            }
+        }
+        // G_h,t[row][jbeg + lane] and [jbeg + 64 + lane]
+        float gv0[ROWS], gv1[ROWS];
+        {
+            unsigned long long w0[ROWS], w1[ROWS];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const bool rv = row0 + r < B;
+                const unsigned long long* rp = slotp + (size_t)(row0 + r) * H3;
+                w0[r] = (rv && v0) ? rec::load_word(rp + j0) : 0ull;
+                w1[r] = (rv && v1) ? rec::load_word(rp + j1) : 0ull;
+            }
+            bool ok = true;
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const bool rv = row0 + r < B;
+                const unsigned long long* rp = slotp + (size_t)(row0 + r) * H3;
+                gv0[r] = (rv && v0) ? rec::wait_word(rp + j0, w0[r], tag, abort_flag, ok) : 0.f;
+                gv1[r] = (rv && v1) ? rec::wait_word(rp + j1, w1[r], tag, abort_flag, ok) : 0.f;
+            }
+            if (!ok) s_abort = 1;
+        }
+        float acc[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r] = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const float gk = jj < 64 ? rec::bcast(gv0[r], jj) : rec::bcast(gv1[r], jj - 64);
+                acc[r] = fmaf(gk, w[jj], acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) part[i & 1][wave][r][lane] = acc[r];
+        __syncthreads();
+        if (s_abort) {
+            aborted = true;
+            break;
+        }
+        if (owner) {
+            float sum = ddirect;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) sum += part[i & 1][w2][wave][lane];
+            dh = sum;
+        }
+    }
+    if (owner) dh0[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : dh;
+}
+
+// ------------------------------------------------------------- config ---
+constexpr int kFwdNK[] = {8, 16, 24, 32};
+constexpr int kBwdNJ[] = {24, 48, 72, 96};
+
+template <int ROWS>
+const void* fwd_ptr(int nk) {
+    switch (nk) {
+        case 8: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<8, ROWS>);
+        case 16: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<16, ROWS>);
+        case 24: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<24, ROWS>);
+        default: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<32, ROWS>);
+    }
+}
+
+template <int ROWS>
+const void* bwd_ptr(int nj) {
+    switch (nj) {
+        case 24: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<24, ROWS>);
+        case 48: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<48, ROWS>);
+        case 72: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<72, ROWS>);
+        default: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<96, ROWS>);
+    }
+}
+
+const void* kernel_ptr(int dir, int cap, int rows) {
+    if (dir == 0) {
+        if (rows == 1) return fwd_ptr<1>(cap);
+        if (rows == 2) return fwd_ptr<2>(cap);
+        return fwd_ptr<4>(cap);
+    }
+    if (rows == 1) return bwd_ptr<1>(cap);
+    if (rows == 2) return bwd_ptr<2>(cap);
+    return bwd_ptr<4>(cap);
+}
+
+// Per-wavefront chunk and the smallest compiled capacity that holds it.
+void chunk_of(int dir, int H, int* chunk, int* cap) {
+    const int len = dir == 0 ? H : 3 * H;
+    *chunk = (len + NW - 1) / NW;
+    *cap = 0;
+    if (dir == 0) {
+        for (int c : kFwdNK)
+            if (c >= *chunk) { *cap = c; break; }
+    } else {
+        for (int c : kBwdNJ)
+            if (c >= *chunk) { *cap = c; break; }
+    }
+}
+
+}  // namespace
+
+int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_rows, RecConfig* cfg) {
+    int chunk = 0, cap = 0;
+    chunk_of(dir, hidden, &chunk, &cap);
+    if (cap == 0) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register-resident recurrence needs hidden_size <= 256");
+    const int S = (hidden + 63) / 64;
+    for (int rows : {1, 2, 4}) {
+        if (fixed_rows && rows != fixed_rows) continue;
+        const int G = (batch + rows - 1) / rows;
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows), NTH, 0) != hipSuccess)
+            continue;
+        if ((long)G * S > (long)per_cu * dev.num_cus) continue;
+        cfg->kind = REC_REGISTER;
+        cfg->groups = G;
+        cfg->slices = S;
+        cfg->units = 64;
+        cfg->rows = rows;
+        cfg->pair_waves = 0;
+        cfg->chunk = chunk;
+        cfg->lds_bytes = 0;
+        return 0;
+    }
+    return fail(RKA_ERR_TOO_LARGE_FOR_RESIDENT_LAUNCH,
+                "register-resident recurrence does not fit resident: batch=" + std::to_string(batch) +
+                    ", hidden=" + std::to_string(hidden));
+}
+
+int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stream) {
+    int chunk = 0, cap = 0;
+    chunk_of(dir, a.H, &chunk, &cap);
+    if (cap == 0 || chunk != c.chunk) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: bad config");
+    const bool aligned = (reinterpret_cast<uintptr_t>(a.w_hh) & 15u) == 0;
+    RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
+                  (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0};
+    const void* k = kernel_ptr(dir, cap, c.rows);
+    if (dir == 0) {
+        void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
+                        (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
+        RKA_RETURN_IF_HIP(hipLaunchCooperativeKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
+    } else {
+        void* args[] = {(void*)&a.dy, (void*)&a.dhn, (void*)&a.reserve, (void*)&a.h0, (void*)&a.y,
+                        (void*)&a.w_hh, (void*)&a.gout, (void*)&a.dh0, (void*)&a.exch, (void*)&a.abort_flag,
+                        (void*)&prm};
+        RKA_RETURN_IF_HIP(hipLaunchCooperativeKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
+    }
+    return 0;
+}
+
+}  // namespace rka

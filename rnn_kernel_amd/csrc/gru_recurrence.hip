@@ -1,483 +1,42 @@
-// Persistent GRU recurrences for gfx950: forward (t = 0..T-1) and BPTT
-// (t = T-1..0), each one cooperative launch that loops over time inside.
+// Recurrence dispatcher: picks the kernel family and decomposition for a
+// shape, zeroes the exchange slots and launches one cooperative kernel.
 //
-// Decomposition (weight-stationary).  The batch is cut into G groups of
-// `rows` sequences and the hidden units into S slices of `units` units; the
-// workgroup (g, s) owns the (row, unit) pairs of that tile for the whole
-// sequence, keeps the W_hh entries those units need in LDS (loaded once), and
-// exchanges per-step state with the other S workgroups of its group only.
-// Workgroup w maps to g = w % G, s = w / G, so with G = 8 every group's
-// workgroups land on one XCD under the round-robin dispatch (placement only
-// affects speed; correctness never depends on it).
-//
-// Synchronisation is flag-in-data: each published value is a 64-bit word
-// {fp32 bits, step tag} written with one agent-scope atomic store and read
-// with agent-scope atomic loads, so a reader needs a single round trip per
-// step and no separate barrier counter.  Two slots (step parity) suffice: a
-// writer can only reach step t+2 after every reader of its group has
-// published step t+1, i.e. after it finished reading step t.  Spins are
-// bounded; on time-out a device flag is raised, every workgroup leaves its
-// time loop and the final state is written as NaN.
-//
-// Forward, per step t (pairs (b,u) of the tile; gates r, z, n):
-//   a = W_hh h_{t-1} + b_hh; r = sigmoid(gx_r + a_r); z = sigmoid(gx_z + a_z);
-//   n = tanh(gx_n + r a_n); h_t = n + z (h_{t-1} - n)
-//   reserve[b,t] = (r, z, n, a_n)        (src/rnn_kernel/a100/prod/kernels/
-//                                          a100_gru_h256_kernels.cu:756-776)
-// Backward, per step t with g = dh_t + dy_t:
-//   dz = g (h_{t-1} - n), dn^ = g (1 - z)(1 - n^2), dr^ = dn^ a_n r (1 - r),
-//   dz^ = dz z (1 - z), da_n = dn^ r; dh_{t-1} = g z + G_h W_hh
-//   (a100_gru_h256_kernels.cu:842-866,915-932).  The gate gradients are
-//   written as g_out[b,t] = (da_n, dr^, dz^, dn^) so that G_i = columns
-//   [H,4H) and G_h = rotation of columns [0,3H) are both contiguous ranges.
-#include "rka_internal.h"
+// Families (both persistent, one launch per layer and direction, the time
+// loop inside the kernel, workgroups co-resident by cooperative launch):
+//   register-resident (gru_rec_reg.hip)  hidden <= 256, W_hh slice in VGPRs;
+//   LDS-tiled         (gru_rec_tiled.hip) any hidden whose tile fits LDS.
+#include "rec_common.h"
 
-#include <algorithm>
-#include <cmath>
 #include <mutex>
-#include <vector>
 
 namespace rka {
 
-int g_override_units[2] = {0, 0};
-int g_override_pair_waves[2] = {0, 0};
-
 namespace {
-
-constexpr int NW = 8;          // wavefronts per workgroup
-constexpr int NTH = NW * 64;   // threads per workgroup
-constexpr int SPIN_LIMIT = 1 << 21;
-
-struct RecParams {
-    int B, T, H;
-    int G, S, U, Bg;   // groups, slices, units per slice, rows per group
-    int RP;            // padded LDS row length (floats) of the exchanged rows
-    int KCH;           // k-chunk per wavefront (multiple of 4)
-    int KLEN;          // dot-product length rounded up to 4 (H fwd, 3H bwd)
+std::mutex g_override_mutex;
+struct Override {
+    int kind = 0, units = 0, param = 0;
 };
-
-__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
-
-__device__ __forceinline__ unsigned long long pack_word(float v, unsigned tag) {
-    return ((unsigned long long)tag << 32) | (unsigned long long)__float_as_uint(v);
-}
-
-__device__ __forceinline__ unsigned long long load_word(const unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_word(unsigned long long* p, unsigned long long w) {
-    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Gathers `nrows` rows of `len` published words with step tag `tag` from
-// src (row stride `len`) into LDS rows of stride RP.  Returns false when the
-// spin budget ran out or another workgroup raised the abort flag.
-__device__ bool gather_rows(const unsigned long long* __restrict__ src, int nrows, int len, unsigned tag,
-                            float* __restrict__ dst, int RP, int* __restrict__ abort_flag) {
-    const int total = nrows * len;
-    bool ok = true;
-    for (int base = 0; base < total; base += NTH * 4) {
-        unsigned long long w[4];
-        int idx[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            idx[j] = base + j * NTH + (int)threadIdx.x;
-            w[j] = idx[j] < total ? load_word(src + idx[j]) : 0ull;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (idx[j] >= total) continue;
-            int spins = 0;
-            while ((unsigned)(w[j] >> 32) != tag) {
-                if (!ok) break;
-                if (++spins > SPIN_LIMIT) {
-                    __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    ok = false;
-                    break;
-                }
-                if ((spins & 1023) == 0 &&
-                    __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-                    ok = false;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-                w[j] = load_word(src + idx[j]);
-            }
-            const int r = idx[j] / len;
-            const int k = idx[j] - r * len;
-            dst[r * RP + k] = __uint_as_float((unsigned)w[j]);
-        }
-    }
-    return ok;
-}
-
-// ------------------------------------------------------------- forward ---
-template <int PW>
-__global__ __launch_bounds__(NTH) void gru_rec_forward_kernel(
-    const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
-    const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
-    float* __restrict__ reserve, unsigned long long* __restrict__ exch, int* __restrict__ abort_flag,
-    RecParams p) {
-    constexpr int KC = NW / PW;
-    constexpr int NP = 64 * PW;  // pair slots per workgroup
-    extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ int s_abort;
-
-    const int B = p.B, T = p.T, H = p.H, RP = p.RP;
-    float* Wl = lds;                         // [U][3][RP]  W_hh rows of the slice's units
-    float* hl = Wl + p.U * 3 * RP;           // [Bg][RP]    h_{t-1} of the group's rows
-    float* part = hl + p.Bg * RP;            // [2][KC][3][NP]
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int pw = wave % PW;
-    const int kc = wave / PW;
-    const int g = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
-    const int pair = pw * 64 + lane;
-    const int bl = pair / p.U;
-    const int ul = pair - bl * p.U;
-    const int b = g * p.Bg + bl;
-    const int u = s * p.U + ul;
-    const bool slot = bl < p.Bg;
-    const bool valid = slot && b < B && u < H;
-    const bool owner = valid && kc == 0;
-    const int row0 = g * p.Bg;
-    const int nrows = max(0, min(p.Bg, B - row0));
-
-    for (int idx = tid; idx < p.U * 3 * RP; idx += NTH) {
-        const int k = idx % RP;
-        const int rest = idx / RP;
-        const int gate = rest % 3;
-        const int unit = s * p.U + rest / 3;
-        Wl[idx] = (k < H && unit < H) ? w_hh[(size_t)(gate * H + unit) * H + k] : 0.f;
-    }
-    for (int idx = tid; idx < p.Bg * RP; idx += NTH) {
-        const int r = idx / RP;
-        const int k = idx - r * RP;
-        hl[idx] = (r < nrows && k < H) ? h0[(size_t)(row0 + r) * H + k] : 0.f;
-    }
-    if (tid == 0) s_abort = 0;
-
-    float h_prev = 0.f, bias_r = 0.f, bias_z = 0.f, bias_n = 0.f;
-    float gxr = 0.f, gxz = 0.f, gxn = 0.f;
-    if (owner) {
-        h_prev = h0[(size_t)b * H + u];
-        bias_r = b_hh[u];
-        bias_z = b_hh[H + u];
-        bias_n = b_hh[2 * H + u];
-        const float* gp = gx + (size_t)b * T * 3 * H;
-        gxr = gp[u];
-        gxz = gp[H + u];
-        gxn = gp[2 * H + u];
-    }
-    const int kbeg = kc * p.KCH;
-    const int kend = min(p.KLEN, kbeg + p.KCH);
-    const float* wr = Wl + (ul * 3) * RP;
-    const float* hrow = hl + bl * RP;
-    bool aborted = false;
-    __syncthreads();
-
-    for (int t = 0; t < T; ++t) {
-        if (t > 0) {
-            const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H + (size_t)row0 * H;
-            if (!gather_rows(src, nrows, H, (unsigned)t, hl, RP, abort_flag)) s_abort = 1;
-            __syncthreads();
-        }
-        float ar = 0.f, az = 0.f, an = 0.f;
-        if (slot) {
-            for (int k = kbeg; k < kend; k += 4) {
-                const float4 hv = *reinterpret_cast<const float4*>(hrow + k);
-                const float4 w0 = *reinterpret_cast<const float4*>(wr + k);
-                const float4 w1 = *reinterpret_cast<const float4*>(wr + RP + k);
-                const float4 w2 = *reinterpret_cast<const float4*>(wr + 2 * RP + k);
-                ar = fmaf(hv.x, w0.x, ar); ar = fmaf(hv.y, w0.y, ar);
-                ar = fmaf(hv.z, w0.z, ar); ar = fmaf(hv.w, w0.w, ar);
-                az = fmaf(hv.x, w1.x, az); az = fmaf(hv.y, w1.y, az);
-                az = fmaf(hv.z, w1.z, az); az = fmaf(hv.w, w1.w, az);
-                an = fmaf(hv.x, w2.x, an); an = fmaf(hv.y, w2.y, an);
-                an = fmaf(hv.z, w2.z, an); an = fmaf(hv.w, w2.w, an);
-            }
-        }
-        float* pp = part + ((t & 1) * KC + kc) * 3 * NP;
-        pp[pair] = ar;
-        pp[NP + pair] = az;
-        pp[2 * NP + pair] = an;
-        __syncthreads();
-        if (s_abort) {
-            aborted = true;
-            break;
-        }
-        if (owner) {
-            float sr = bias_r, sz = bias_z, sn = bias_n;
-            const float* pb = part + (t & 1) * KC * 3 * NP;
-#pragma unroll
-            for (int c = 0; c < KC; ++c) {
-                sr += pb[c * 3 * NP + pair];
-                sz += pb[c * 3 * NP + NP + pair];
-                sn += pb[c * 3 * NP + 2 * NP + pair];
-            }
-            const float r = sigmoid_f(gxr + sr);
-            const float z = sigmoid_f(gxz + sz);
-            const float n = tanhf(gxn + r * sn);
-            const float h = n + z * (h_prev - n);
-            store_word(exch + (size_t)(t & 1) * B * H + (size_t)b * H + u, pack_word(h, (unsigned)(t + 1)));
-            const size_t bt = (size_t)b * T + t;
-            y[bt * H + u] = h;
-            if (reserve) {
-                float* cp = reserve + bt * 4 * H;
-                cp[u] = r;
-                cp[H + u] = z;
-                cp[2 * H + u] = n;
-                cp[3 * H + u] = sn;
-            }
-            h_prev = h;
-            if (t + 1 < T) {
-                const float* gp = gx + (bt + 1) * 3 * H;
-                gxr = gp[u];
-                gxz = gp[H + u];
-                gxn = gp[2 * H + u];
-            }
-        }
-    }
-    if (owner) hn[(size_t)b * H + u] = aborted ? __builtin_nanf("") : h_prev;
-}
-
-// ------------------------------------------------------------ backward ---
-template <int PW>
-__global__ __launch_bounds__(NTH) void gru_rec_backward_kernel(
-    const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
-    const float* __restrict__ h0, const float* __restrict__ y, const float* __restrict__ w_hh,
-    float* __restrict__ gout, float* __restrict__ dh0, unsigned long long* __restrict__ exch,
-    int* __restrict__ abort_flag, RecParams p) {
-    constexpr int KC = NW / PW;
-    constexpr int NP = 64 * PW;
-    extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ int s_abort;
-
-    const int B = p.B, T = p.T, H = p.H, RP = p.RP;
-    const int H3 = 3 * H;
-    float* Wt = lds;                    // [U][RP]   column u of W_hh, all 3H gate rows
-    float* gl = Wt + p.U * RP;          // [Bg][RP]  G_h,t rows of the group (r, z, n order)
-    float* part = gl + p.Bg * RP;       // [2][KC][NP]
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int pw = wave % PW;
-    const int kc = wave / PW;
-    const int g = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
-    const int pair = pw * 64 + lane;
-    const int bl = pair / p.U;
-    const int ul = pair - bl * p.U;
-    const int b = g * p.Bg + bl;
-    const int u = s * p.U + ul;
-    const bool slot = bl < p.Bg;
-    const bool valid = slot && b < B && u < H;
-    const bool owner = valid && kc == 0;
-    const int row0 = g * p.Bg;
-    const int nrows = max(0, min(p.Bg, B - row0));
-
-    for (int idx = tid; idx < p.U * RP; idx += NTH) {
-        const int j = idx % RP;
-        const int unit = s * p.U + idx / RP;
-        Wt[idx] = (j < H3 && unit < H) ? w_hh[(size_t)j * H + unit] : 0.f;
-    }
-    for (int idx = tid; idx < p.Bg * RP; idx += NTH) gl[idx] = 0.f;
-    if (tid == 0) s_abort = 0;
-
-    float dh = 0.f;
-    float dyv = 0.f, cr = 0.f, cz = 0.f, cn = 0.f, ca = 0.f, hp = 0.f;
-    if (owner) {
-        if (dhn) dh = dhn[(size_t)b * H + u];
-        const size_t bt = (size_t)b * T + (T - 1);
-        if (dy) dyv = dy[bt * H + u];
-        const float* cp = reserve + bt * 4 * H;
-        cr = cp[u]; cz = cp[H + u]; cn = cp[2 * H + u]; ca = cp[3 * H + u];
-        hp = (T > 1) ? y[(bt - 1) * H + u] : h0[(size_t)b * H + u];
-    }
-    const int kbeg = kc * p.KCH;
-    const int kend = min(p.KLEN, kbeg + p.KCH);
-    const float* wrow = Wt + ul * RP;
-    const float* grow = gl + bl * RP;
-    bool aborted = false;
-    float ddirect = 0.f;
-    __syncthreads();
-
-    for (int i = 0; i < T; ++i) {
-        const int t = T - 1 - i;
-        unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
-        if (owner) {
-            const float gsum = dh + dyv;
-            const float dz = gsum * (hp - cn);
-            const float dnh = gsum * (1.0f - cz) * (1.0f - cn * cn);
-            const float dan = dnh * cr;
-            const float drh = dnh * ca * cr * (1.0f - cr);
-            const float dzh = dz * cz * (1.0f - cz);
-            ddirect = gsum * cz;
-            const unsigned tag = (unsigned)(i + 1);
-            unsigned long long* wp = slotp + (size_t)b * H3 + u;
-            store_word(wp, pack_word(drh, tag));
-            store_word(wp + H, pack_word(dzh, tag));
-            store_word(wp + 2 * H, pack_word(dan, tag));
-            const size_t bt = (size_t)b * T + t;
-            float* op = gout + bt * 4 * H;
-            op[u] = dan;
-            op[H + u] = drh;
-            op[2 * H + u] = dzh;
-            op[3 * H + u] = dnh;
-            if (t > 0) {
-                const size_t pbt = bt - 1;
-                dyv = dy ? dy[pbt * H + u] : 0.f;
-                const float* cp = reserve + pbt * 4 * H;
-                cr = cp[u]; cz = cp[H + u]; cn = cp[2 * H + u]; ca = cp[3 * H + u];
-                hp = (t > 1) ? y[(pbt - 1) * H + u] : h0[(size_t)b * H + u];
-            }
-        }
-        if (!gather_rows(slotp + (size_t)row0 * H3, nrows, H3, (unsigned)(i + 1), gl, RP, abort_flag))
-            s_abort = 1;
-        __syncthreads();
-        float acc = 0.f;
-        if (slot) {
-            for (int k = kbeg; k < kend; k += 4) {
-                const float4 gv = *reinterpret_cast<const float4*>(grow + k);
-                const float4 wv = *reinterpret_cast<const float4*>(wrow + k);
-                acc = fmaf(gv.x, wv.x, acc); acc = fmaf(gv.y, wv.y, acc);
-                acc = fmaf(gv.z, wv.z, acc); acc = fmaf(gv.w, wv.w, acc);
-            }
-        }
-        part[((i & 1) * KC + kc) * NP + pair] = acc;
-        __syncthreads();
-        if (s_abort) {
-            aborted = true;
-            break;
-        }
-        if (owner) {
-            float sum = ddirect;
-            const float* pb = part + (i & 1) * KC * NP;
-#pragma unroll
-            for (int c = 0; c < KC; ++c) sum += pb[c * NP + pair];
-            dh = sum;
-        }
-    }
-    if (owner) dh0[(size_t)b * H + u] = aborted ? __builtin_nanf("") : dh;
-}
-
-__global__ void fill_u64_kernel(unsigned long long* __restrict__ p, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = 0ull;
-}
-
-// ------------------------------------------------------------ config ---
-int rows_padded(int len) {
-    // Row stride = len rounded up to 64 floats plus 4: consecutive rows start
-    // 4 banks apart, so the b128 reads of distinct rows do not conflict.
-    return (len + 63) / 64 * 64 + 4;
-}
-
-int lds_bytes_for(int dir, int H, int U, int Bg, int PW) {
-    const int KC = NW / PW;
-    const int NP = 64 * PW;
-    if (dir == 0) {
-        const int RP = rows_padded(H);
-        return (U * 3 * RP + Bg * RP + 2 * KC * 3 * NP) * 4;
-    }
-    const int RP = rows_padded(3 * H);
-    return (U * RP + Bg * RP + 2 * KC * NP) * 4;
-}
-
-const void* kernel_ptr(int dir, int PW) {
-    if (dir == 0) {
-        if (PW == 1) return reinterpret_cast<const void*>(&gru_rec_forward_kernel<1>);
-        if (PW == 2) return reinterpret_cast<const void*>(&gru_rec_forward_kernel<2>);
-        return reinterpret_cast<const void*>(&gru_rec_forward_kernel<4>);
-    }
-    if (PW == 1) return reinterpret_cast<const void*>(&gru_rec_backward_kernel<1>);
-    if (PW == 2) return reinterpret_cast<const void*>(&gru_rec_backward_kernel<2>);
-    return reinterpret_cast<const void*>(&gru_rec_backward_kernel<4>);
-}
-
-int max_resident(const DeviceInfo& dev, int dir, int PW, int lds) {
-    const void* k = kernel_ptr(dir, PW);
-    if (lds > 65536) {
-        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) return 0;
-    }
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NTH, lds) != hipSuccess) return 0;
-    return per_cu * dev.num_cus;
-}
-
-RecParams make_params(int dir, int B, int T, int H, const RecConfig& c) {
-    RecParams p{};
-    p.B = B;
-    p.T = T;
-    p.H = H;
-    p.G = c.groups;
-    p.S = c.slices;
-    p.U = c.units;
-    p.Bg = c.rows;
-    const int len = dir == 0 ? H : 3 * H;
-    p.RP = rows_padded(len);
-    p.KLEN = (len + 3) / 4 * 4;
-    const int KC = NW / c.pair_waves;
-    p.KCH = ((p.KLEN + KC - 1) / KC + 3) / 4 * 4;
-    return p;
-}
-
+Override g_override[2];
 }  // namespace
 
+void set_rec_override(int dir, int kind, int units, int param) {
+    std::lock_guard<std::mutex> lock(g_override_mutex);
+    g_override[dir] = Override{kind, units, param};
+}
+
 int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, RecConfig* cfg) {
-    const int ncu = dev.num_cus > 0 ? dev.num_cus : 256;
-    const int lds_cap = dev.max_lds_per_block > 0 ? dev.max_lds_per_block : 65536;
-    const int fixed_u = g_override_units[dir];
-    const int fixed_pw = g_override_pair_waves[dir];
-    bool found = false;
-    double best = 0;
-    RecConfig best_cfg{};
-    for (int PW : {1, 2, 4}) {
-        if (fixed_pw && PW != fixed_pw) continue;
-        for (int U : {8, 4, 16, 2, 32, 1, 64}) {
-            if (fixed_u && U != fixed_u) continue;
-            const int Bg = std::min(PW * (64 / U), batch);
-            if (Bg < 1) continue;
-            // Only use PW > 1 when its extra rows are needed.
-            if (PW > 1 && (PW / 2) * (64 / U) >= batch && !fixed_pw) continue;
-            const int G = (batch + Bg - 1) / Bg;
-            const int S = (hidden + U - 1) / U;
-            const int lds = lds_bytes_for(dir, hidden, U, Bg, PW);
-            if (lds > lds_cap) continue;
-            const int nwg = G * S;
-            const int cap = max_resident(dev, dir, PW, lds);
-            if (nwg > cap) continue;
-            // Per-step cost model: per-workgroup dot work, times the number of
-            // workgroups that share a CU, plus a term for the exchange volume.
-            const double work = (double)Bg * U * hidden * 3.0 / (64.0 * PW);
-            const double share = std::ceil((double)nwg / ncu);
-            const double xfer = (double)Bg * hidden * (dir == 0 ? 1 : 3) / NTH;
-            double score = work * share + 4.0 * xfer;
-            if (G % 8 == 0 || G == 1) score *= 0.98;  // whole groups per XCD
-            if (!found || score < best) {
-                found = true;
-                best = score;
-                best_cfg.groups = G;
-                best_cfg.slices = S;
-                best_cfg.units = U;
-                best_cfg.rows = Bg;
-                best_cfg.pair_waves = PW;
-                best_cfg.lds_bytes = lds;
-            }
-        }
+    Override o;
+    {
+        std::lock_guard<std::mutex> lock(g_override_mutex);
+        o = g_override[dir];
     }
-    if (!found) {
-        return fail(RKA_ERR_TOO_LARGE_FOR_RESIDENT_LAUNCH,
-                    "no resident decomposition of the " + std::string(dir == 0 ? "forward" : "backward") +
-                        " recurrence fits: batch=" + std::to_string(batch) + ", hidden=" + std::to_string(hidden));
+    if (o.kind == REC_TILED) return tiled_choose(dir, batch, hidden, dev, o.units, o.param, cfg);
+    if (o.kind == REC_REGISTER) return reg_choose(dir, batch, hidden, dev, o.param, cfg);
+    if (hidden <= 256 && reg_choose(dir, batch, hidden, dev, 0, cfg) == 0) {
+        clear_error();
+        return 0;
     }
-    *cfg = best_cfg;
-    return 0;
+    return tiled_choose(dir, batch, hidden, dev, 0, 0, cfg);
 }
 
 size_t rec_workspace_bytes(int batch, int hidden) {
@@ -488,25 +47,30 @@ size_t rec_workspace_bytes(int batch, int hidden) {
 
 namespace {
 
-int launch_rec(int dir, const RecConfig& c, const RecParams& prm, void** args, void* ws, size_t ws_bytes,
-               hipStream_t stream) {
-    const size_t exch_words = (size_t)2 * prm.B * (dir == 0 ? prm.H : 3 * prm.H);
-    const size_t need = rec_workspace_bytes(prm.B, prm.H);
+__global__ void fill_u64_kernel(unsigned long long* __restrict__ p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0ull;
+}
+
+int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, hipStream_t stream) {
+    const DeviceInfo* dev = nullptr;
+    RKA_RETURN_IF_ERR(current_device_info(&dev));
+    RecConfig c{};
+    RKA_RETURN_IF_ERR(choose_rec_config(dir, a.B, a.H, *dev, &c));
+    const size_t need = rec_workspace_bytes(a.B, a.H);
     if (ws == nullptr || ws_bytes < need)
         return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "recurrence workspace too small: need " + std::to_string(need) +
                                                      " bytes, got " + std::to_string(ws_bytes));
-    (void)exch_words;
+    // Tags start at 1, so zeroed slots never match; a fill kernel (not a
+    // memset node) keeps the sequence capturable in a HIP graph.
     const size_t zero_words = need / sizeof(unsigned long long);
     hipLaunchKernelGGL(fill_u64_kernel, dim3(std::min<size_t>((zero_words + 255) / 256, 1024)), dim3(256), 0,
                        stream, reinterpret_cast<unsigned long long*>(ws), zero_words);
     RKA_RETURN_IF_HIP(hipGetLastError());
-    const void* k = kernel_ptr(dir, c.pair_waves);
-    if (c.lds_bytes > 65536) {
-        RKA_RETURN_IF_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes));
-    }
-    RKA_RETURN_IF_HIP(hipLaunchCooperativeKernel(k, dim3(c.groups * c.slices), dim3(NTH), args,
-                                                 (unsigned)c.lds_bytes, stream));
-    return 0;
+    a.exch = reinterpret_cast<unsigned long long*>(ws);
+    a.abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + need - 256);
+    if (c.kind == REC_REGISTER) return reg_launch(dir, c, a, stream);
+    return tiled_launch(dir, c, a, stream);
 }
 
 }  // namespace
@@ -514,32 +78,37 @@ int launch_rec(int dir, const RecConfig& c, const RecParams& prm, void** args, v
 int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
                        float* y, float* hn, float* reserve, void* ws, size_t ws_bytes,
                        int B, int T, int H, hipStream_t stream) {
-    const DeviceInfo* dev = nullptr;
-    RKA_RETURN_IF_ERR(current_device_info(&dev));
-    RecConfig c{};
-    RKA_RETURN_IF_ERR(choose_rec_config(0, B, H, *dev, &c));
-    RecParams prm = make_params(0, B, T, H, c);
-    unsigned long long* exch = reinterpret_cast<unsigned long long*>(ws);
-    int* abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + rec_workspace_bytes(B, H) - 256);
-    void* args[] = {(void*)&gx, (void*)&h0, (void*)&w_hh, (void*)&b_hh, (void*)&y, (void*)&hn,
-                    (void*)&reserve, (void*)&exch, (void*)&abort_flag, (void*)&prm};
-    return launch_rec(0, c, prm, args, ws, ws_bytes, stream);
+    rec::Args a;
+    a.gx = gx;
+    a.h0 = h0;
+    a.w_hh = w_hh;
+    a.b_hh = b_hh;
+    a.y = y;
+    a.hn = hn;
+    a.reserve = reserve;
+    a.B = B;
+    a.T = T;
+    a.H = H;
+    return launch(0, a, ws, ws_bytes, stream);
 }
 
 int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,
                         const float* h0, const float* y, const float* w_hh,
                         float* g, float* dh0, void* ws, size_t ws_bytes,
                         int B, int T, int H, hipStream_t stream) {
-    const DeviceInfo* dev = nullptr;
-    RKA_RETURN_IF_ERR(current_device_info(&dev));
-    RecConfig c{};
-    RKA_RETURN_IF_ERR(choose_rec_config(1, B, H, *dev, &c));
-    RecParams prm = make_params(1, B, T, H, c);
-    unsigned long long* exch = reinterpret_cast<unsigned long long*>(ws);
-    int* abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + rec_workspace_bytes(B, H) - 256);
-    void* args[] = {(void*)&dy, (void*)&dhn, (void*)&reserve, (void*)&h0, (void*)&y, (void*)&w_hh,
-                    (void*)&g, (void*)&dh0, (void*)&exch, (void*)&abort_flag, (void*)&prm};
-    return launch_rec(1, c, prm, args, ws, ws_bytes, stream);
+    rec::Args a;
+    a.dy = dy;
+    a.dhn = dhn;
+    a.reserve = const_cast<float*>(reserve);
+    a.h0 = h0;
+    a.y = const_cast<float*>(y);
+    a.w_hh = w_hh;
+    a.gout = g;
+    a.dh0 = dh0;
+    a.B = B;
+    a.T = T;
+    a.H = H;
+    return launch(1, a, ws, ws_bytes, stream);
 }
 
 }  // namespace rka

@@ -290,33 +290,37 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn, const float* 
                                seq_len, hidden_size, reinterpret_cast<hipStream_t>(stream));
 }
 
-int rka_set_recurrence_config(int fwd_units, int fwd_pair_waves, int bwd_units, int bwd_pair_waves) {
+int rka_set_recurrence_config(int dir, int kind, int units, int param) {
     clear_error();
-    auto ok_u = [](int u) { return u == 0 || (u > 0 && u <= 64 && (64 % u) == 0); };
-    auto ok_pw = [](int p) { return p == 0 || p == 1 || p == 2 || p == 4; };
-    if (!ok_u(fwd_units) || !ok_u(bwd_units) || !ok_pw(fwd_pair_waves) || !ok_pw(bwd_pair_waves))
-        return fail(RKA_ERR_INVALID_ARGUMENT, "units must divide 64 and pair_waves be 1, 2 or 4 (0 = auto)");
-    g_override_units[0] = fwd_units;
-    g_override_units[1] = bwd_units;
-    g_override_pair_waves[0] = fwd_pair_waves;
-    g_override_pair_waves[1] = bwd_pair_waves;
+    if (dir != 0 && dir != 1) return fail(RKA_ERR_INVALID_ARGUMENT, "dir must be 0 or 1");
+    if (kind == REC_AUTO) {
+        set_rec_override(dir, 0, 0, 0);
+        return 0;
+    }
+    const bool ok_p = param == 0 || param == 1 || param == 2 || param == 4;
+    if (kind == REC_TILED) {
+        if (!(units == 0 || (units > 0 && units <= 64 && (64 % units) == 0)) || !ok_p)
+            return fail(RKA_ERR_INVALID_ARGUMENT, "tiled: units must divide 64, pair_waves be 1, 2 or 4 (0 = auto)");
+    } else if (kind == REC_REGISTER) {
+        if (!ok_p) return fail(RKA_ERR_INVALID_ARGUMENT, "register: rows must be 1, 2 or 4 (0 = auto)");
+        units = 0;
+    } else {
+        return fail(RKA_ERR_INVALID_ARGUMENT, "kind must be 0 (auto), 1 (tiled) or 2 (register)");
+    }
+    set_rec_override(dir, kind, units, param);
     return 0;
 }
 
-int rka_describe_recurrence(int dir, int batch, int hidden_size, int out6[6]) {
+int rka_describe_recurrence(int dir, int batch, int hidden_size, int out8[8]) {
     clear_error();
-    if ((dir != 0 && dir != 1) || !out6) return fail(RKA_ERR_INVALID_ARGUMENT, "dir must be 0 or 1");
+    if ((dir != 0 && dir != 1) || !out8) return fail(RKA_ERR_INVALID_ARGUMENT, "dir must be 0 or 1");
     RKA_RETURN_IF_ERR(check_dims(batch, 1, 1, hidden_size));
     const DeviceInfo* dev = nullptr;
     RKA_RETURN_IF_ERR(current_device_info(&dev));
     RecConfig c{};
     RKA_RETURN_IF_ERR(choose_rec_config(dir, batch, hidden_size, *dev, &c));
-    out6[0] = c.groups;
-    out6[1] = c.slices;
-    out6[2] = c.units;
-    out6[3] = c.rows;
-    out6[4] = c.pair_waves;
-    out6[5] = c.lds_bytes;
+    const int v[8] = {c.kind, c.groups, c.slices, c.units, c.rows, c.pair_waves, c.chunk, c.lds_bytes};
+    for (int i = 0; i < 8; ++i) out8[i] = v[i];
     return 0;
 }
 

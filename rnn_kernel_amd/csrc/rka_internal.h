@@ -75,15 +75,21 @@ size_t splitk_partial_floats(int m, int n, int ksplit);
 int choose_ksplit(int m, int n, int k, int num_cus);
 
 // ----------------------------------------------------------- recurrence ---
+enum RecKind { REC_AUTO = 0, REC_TILED = 1, REC_REGISTER = 2 };
+
 struct RecConfig {
+    int kind = 0;          // REC_TILED or REC_REGISTER
     int groups = 0;        // batch-row groups
     int slices = 0;        // hidden-unit slices
-    int units = 0;         // hidden units per slice (divides 64)
+    int units = 0;         // hidden units per slice
     int rows = 0;          // batch rows per group
-    int pair_waves = 0;    // wavefronts holding (row, unit) pairs
-    int lds_bytes = 0;
+    int pair_waves = 0;    // tiled: wavefronts holding (row, unit) pairs
+    int chunk = 0;         // register: k (forward) / j (backward) values per wavefront
+    int lds_bytes = 0;     // dynamic LDS (tiled) or 0
 };
 int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, RecConfig* cfg);
+// Per-direction override used by rka_set_recurrence_config: kind, units, param.
+void set_rec_override(int dir, int kind, int units, int param);
 
 size_t rec_workspace_bytes(int batch, int hidden);
 
@@ -94,8 +100,5 @@ int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,
                         const float* h0, const float* y, const float* w_hh,
                         float* g, float* dh0, void* ws, size_t ws_bytes,
                         int B, int T, int H, hipStream_t stream);
-
-extern int g_override_units[2];
-extern int g_override_pair_waves[2];
 
 }  // namespace rka

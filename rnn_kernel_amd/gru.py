@@ -159,6 +159,9 @@ class GRUFunction(torch.autograd.Function):
         x, h0, weight_ih, weight_hh, output, h_n, reserve = _run_forward(
             x, h0, weight_ih, weight_hh, bias_ih, bias_hh, training=True)
         ctx.save_for_backward(x, h0, weight_ih, weight_hh, output, reserve)
+        # An unused output's gradient arrives as None (passed to the kernels
+        # as NULL) instead of a materialised zero tensor.
+        ctx.set_materialize_grads(False)
         return output, h_n
 
     @staticmethod

@@ -107,11 +107,26 @@ def _layer_inputs(B, T, I, H, seed, h0_scale=1.0):
     return p, x, h0, dy, dhn
 
 
-@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES)
-def test_layer_forward_backward_matches_oracle(gpu, oracle, B, T, I, H):
-    from rnn_kernel_amd import GRUFunction
+@pytest.fixture(params=["auto", "tiled"])
+def rec_kind(request, hip_lib):
+    """Run a test with the automatic recurrence choice (register-resident for
+    H <= 256) and again with the LDS-tiled kernels forced."""
+    from rnn_kernel_amd import _lib
 
-    print(f"layer vs oracle B={B} T={T} I={I} H={H}", flush=True)
+    if request.param == "tiled":
+        for d in (0, 1):
+            _lib.set_recurrence_config(d, 1, 0, 0)
+    yield request.param
+    for d in (0, 1):
+        _lib.set_recurrence_config(d, 0, 0, 0)
+
+
+@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512)])
+def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
+    from rnn_kernel_amd import GRUFunction, _lib
+
+    print(f"layer vs oracle B={B} T={T} I={I} H={H} kind={rec_kind} "
+          f"fwd={_lib.describe_recurrence(0, B, H)} bwd={_lib.describe_recurrence(1, B, H)}", flush=True)
     p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B * 1000 + T * 10 + H)
     f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
                        p["bias_ih"].numpy(), p["bias_hh"].numpy())
@@ -249,10 +264,10 @@ def test_repeat_runs_are_bitwise_identical(gpu):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("fwd_units,bwd_units", [(1, 1), (4, 16), (64, 2)])
-def test_alternative_decompositions_agree(gpu, hip_lib, fwd_units, bwd_units):
-    """Other (units, pair-wave) tilings of the recurrences give the same answer."""
-    from rnn_kernel_amd import GRU
+@pytest.mark.parametrize("kind,units,param", [(1, 1, 0), (1, 4, 0), (1, 16, 2), (1, 64, 0), (2, 0, 2), (2, 0, 4)])
+def test_alternative_decompositions_agree(gpu, hip_lib, kind, units, param):
+    """Other tilings / kernel families of the recurrences give the same answer."""
+    from rnn_kernel_amd import GRU, _lib
 
     torch.manual_seed(5)
     model = GRU(24, 72).to(gpu)
@@ -266,11 +281,14 @@ def test_alternative_decompositions_agree(gpu, hip_lib, fwd_units, bwd_units):
         return [y.detach().clone(), xi.grad.clone()] + [p.grad.clone() for p in model.parameters()]
 
     base = run()
-    assert hip_lib.rka_set_recurrence_config(fwd_units, 0, bwd_units, 0) == 0
+    for d in (0, 1):
+        _lib.set_recurrence_config(d, kind, units, param)
     try:
+        print("alt", _lib.describe_recurrence(0, 10, 72), _lib.describe_recurrence(1, 10, 72), flush=True)
         alt = run()
     finally:
-        hip_lib.rka_set_recurrence_config(0, 0, 0, 0)
+        for d in (0, 1):
+            _lib.set_recurrence_config(d, 0, 0, 0)
     for a, b in zip(base, alt):
         assert _rel(a, b) <= 1e-5
 

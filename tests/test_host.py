@@ -56,8 +56,11 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     assert "must be >= 1" in _lib.last_error()
     rc = hip_lib.rka_gru_forward(*([None] * 10), 0, 2, 8, 4, 4, None)
     assert rc == 1001 and "null tensor pointer" in _lib.last_error()
-    assert hip_lib.rka_set_recurrence_config(3, 0, 0, 0) == 1001
-    assert hip_lib.rka_set_recurrence_config(0, 3, 0, 0) == 1001
+    assert hip_lib.rka_set_recurrence_config(2, 0, 0, 0) == 1001   # bad direction
+    assert hip_lib.rka_set_recurrence_config(0, 3, 0, 0) == 1001   # bad kind
+    assert hip_lib.rka_set_recurrence_config(0, 1, 3, 0) == 1001   # units must divide 64
+    assert hip_lib.rka_set_recurrence_config(1, 2, 0, 3) == 1001   # rows 1, 2 or 4
+    assert hip_lib.rka_set_recurrence_config(0, 0, 0, 0) == 0
 
 
 def test_module_construction_and_validation_messages():
