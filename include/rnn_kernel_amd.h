@@ -143,7 +143,7 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
  * kind 1: LDS-tiled; units = hidden units per workgroup (a divisor of 64,
  *         0 = auto), param = wavefronts holding (row, unit) pairs (1, 2, 4,
  *         0 = auto);
- * kind 2: register-resident; units ignored, param = batch rows per
+ * kind 2: register-resident; units = 64 (or 0), param = batch rows per
  *         workgroup (1, 2, 4, 0 = auto). */
 #define RKA_REC_AUTO 0
 #define RKA_REC_TILED 1
@@ -155,6 +155,11 @@ int rka_set_recurrence_config(int dir, int kind, int units, int param);
  * chunk, lds_bytes}. */
 int rka_describe_recurrence(int dir, int batch, int hidden_size, int out8[8]);
 
+
+/* Evaluates the recurrence kernels' gate nonlinearities (the same device
+ * functions) elementwise: sigmoid_out = sigmoid(x), tanh_out = tanh(x).
+ * For accuracy tests of those functions; no reference counterpart. */
+int rka_eval_gate_functions(const float* x, float* sigmoid_out, float* tanh_out, int n, void* stream);
 
 /*
  * Stage profiler (the native counterpart of the reference's per-phase CUDA

@@ -34,6 +34,7 @@ SIGNATURES = {
     "rka_gru_recurrence_backward": (_I, [_P] * 8 + [_P, _SZ, _I, _I, _I, _P]),
     "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
     "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
+    "rka_eval_gate_functions": (_I, [_P, _P, _P, _I, _P]),
     "rka_profile_enable": (_I, [_I]),
     "rka_profile_read": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "rka_profile_stage_name": (ctypes.c_char_p, [_I]),

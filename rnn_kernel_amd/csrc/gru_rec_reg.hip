@@ -12,7 +12,17 @@
 // readlane into scalar operands and runs the chunk's FMAs without touching
 // LDS; the 8 wavefront partials are reduced in LDS (one barrier per step) and
 // wavefront r applies the gate math of row r.  With 64 units per workgroup a
-// hidden size of 256 needs 4 exchanging workgroups per batch row.
+// hidden size of 256 needs 4 exchanging workgroups per batch row, which sit
+// on one XCD.
+//
+// Alternatives measured slower on MI355X at B=64, H=256, T=512 (kept out):
+//   * 128 units per workgroup (2 exchanging workgroups, but twice the FMAs on
+//     the owner's critical path): forward 1.67 vs 1.29 us/step;
+//   * a ninth, non-polling wavefront for the gate math (it shares a SIMD with
+//     two polling wavefronts): forward 1.6 vs 1.29 us/step;
+//   * backward exchanging per-slice partial sums of dh (forward-sized
+//     exchange, one polling wavefront, but a second barrier and the FMAs
+//     ahead of the publish): 2.56 vs ~2.3 us/step.
 //
 // Forward maths (src/rnn_kernel/a100/prod/kernels/a100_gru_h256_kernels.cu:756-776):
 //   a = W_hh h_{t-1} + b_hh; r = sigmoid(gx_r + a_r); z = sigmoid(gx_z + a_z);
@@ -108,6 +118,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
     const bool kvalid = lane < p.chunk && kk < H;
     bool aborted = false;
     for (int t = 0; t < T; ++t) {
+        // @probe:step_begin
         // h_{t-1}[row][kbeg + lane]
         float hv[ROWS];
         if (t == 0) {
@@ -129,6 +140,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
             }
             if (!ok) s_abort = 1;
         }
+        // @probe:polled
         float ar[ROWS], az[ROWS], an[ROWS];
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) ar[r] = az[r] = an[r] = 0.f;
@@ -148,22 +160,21 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
             part[t & 1][wave][1][r][lane] = az[r];
             part[t & 1][wave][2][r][lane] = an[r];
         }
+        // @probe:computed
         __syncthreads();
+        // @probe:synced
         if (s_abort) {
             aborted = true;
             break;
         }
         if (owner) {
-            float sr = bias_r, sz = bias_z, sn = bias_n;
-#pragma unroll
-            for (int w2 = 0; w2 < NW; ++w2) {
-                sr += part[t & 1][w2][0][wave][lane];
-                sz += part[t & 1][w2][1][wave][lane];
-                sn += part[t & 1][w2][2][wave][lane];
-            }
+            const int pb = t & 1;
+            const float sr = bias_r + rec::tree8([&](int w2) { return part[pb][w2][0][wave][lane]; });
+            const float sz = bias_z + rec::tree8([&](int w2) { return part[pb][w2][1][wave][lane]; });
+            const float sn = bias_n + rec::tree8([&](int w2) { return part[pb][w2][2][wave][lane]; });
             const float r = rec::sigmoid_f(gxr + sr);
             const float z = rec::sigmoid_f(gxz + sz);
-            const float n = tanhf(gxn + r * sn);
+            const float n = rec::tanh_f(gxn + r * sn);
             const float h = n + z * (h_prev - n);
             rec::store_word(exch + (size_t)(t & 1) * B * H + (size_t)prow * H + u, rec::pack_word(h, (unsigned)(t + 1)));
             const size_t bt = (size_t)prow * T + t;
@@ -183,7 +194,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
                 gxn = gp[2 * H + u];
             }
         }
+        // @probe:step_end
     }
+    // @probe:kernel_end
     if (owner) hn[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : h_prev;
 }
 
@@ -240,6 +253,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
     bool aborted = false;
     float ddirect = 0.f;
     for (int i = 0; i < T; ++i) {
+        // @probe:step_begin
         const int t = T - 1 - i;
         unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
         const unsigned tag = (unsigned)(i + 1);
@@ -272,6 +286,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
                 hp = (t > 1) ? y[(pbt - 1) * H + u] : h0[(size_t)prow * H + u];
             }
         }
+        // @probe:published
         // G_h,t[row][jbeg + lane] and [jbeg + 64 + lane]
         float gv0[ROWS], gv1[ROWS];
         {
@@ -293,31 +308,40 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
             }
             if (!ok) s_abort = 1;
         }
+        // @probe:polled
         float acc[ROWS];
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) acc[r] = 0.f;
+        // Blocks of 16 broadcasts keep a block's scalar operands live only
+        // while its FMAs run.
 #pragma unroll
-        for (int jj = 0; jj < NJ; ++jj) {
+        for (int jb = 0; jb < NJ; jb += 16) {
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const float gk = jj < 64 ? rec::bcast(gv0[r], jj) : rec::bcast(gv1[r], jj - 64);
-                acc[r] = fmaf(gk, w[jj], acc[r]);
+            for (int jj = jb; jj < (jb + 16 < NJ ? jb + 16 : NJ); ++jj) {
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    const float gk = jj < 64 ? rec::bcast(gv0[r], jj) : rec::bcast(gv1[r], jj - 64);
+                    acc[r] = fmaf(gk, w[jj], acc[r]);
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) part[i & 1][wave][r][lane] = acc[r];
+        // @probe:computed
         __syncthreads();
+        // @probe:synced
         if (s_abort) {
             aborted = true;
             break;
         }
         if (owner) {
-            float sum = ddirect;
-#pragma unroll
-            for (int w2 = 0; w2 < NW; ++w2) sum += part[i & 1][w2][wave][lane];
-            dh = sum;
+            const int pb = i & 1;
+            dh = ddirect + rec::tree8([&](int w2) { return part[pb][w2][wave][lane]; });
         }
+        // @probe:step_end
     }
+    // @probe:kernel_end
     if (owner) dh0[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : dh;
 }
 
@@ -372,10 +396,13 @@ void chunk_of(int dir, int H, int* chunk, int* cap) {
 
 }  // namespace
 
-int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_rows, RecConfig* cfg) {
+int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_units, int fixed_rows,
+               RecConfig* cfg) {
     int chunk = 0, cap = 0;
     chunk_of(dir, hidden, &chunk, &cap);
     if (cap == 0) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register-resident recurrence needs hidden_size <= 256");
+    if (fixed_units && fixed_units != 64)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "register-resident recurrence uses 64 units per workgroup");
     const int S = (hidden + 63) / 64;
     for (int rows : {1, 2, 4}) {
         if (fixed_rows && rows != fixed_rows) continue;

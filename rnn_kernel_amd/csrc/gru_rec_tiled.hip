@@ -187,7 +187,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
             }
             const float r = sigmoid_f(gxr + sr);
             const float z = sigmoid_f(gxz + sz);
-            const float n = tanhf(gxn + r * sn);
+            const float n = tanh_f(gxn + r * sn);
             const float h = n + z * (h_prev - n);
             store_word(exch + (size_t)(t & 1) * B * H + (size_t)b * H + u, pack_word(h, (unsigned)(t + 1)));
             const size_t bt = (size_t)b * T + t;

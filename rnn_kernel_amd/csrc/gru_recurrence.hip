@@ -31,8 +31,8 @@ int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, Rec
         o = g_override[dir];
     }
     if (o.kind == REC_TILED) return tiled_choose(dir, batch, hidden, dev, o.units, o.param, cfg);
-    if (o.kind == REC_REGISTER) return reg_choose(dir, batch, hidden, dev, o.param, cfg);
-    if (hidden <= 256 && reg_choose(dir, batch, hidden, dev, 0, cfg) == 0) {
+    if (o.kind == REC_REGISTER) return reg_choose(dir, batch, hidden, dev, o.units, o.param, cfg);
+    if (hidden <= 256 && reg_choose(dir, batch, hidden, dev, 0, 0, cfg) == 0) {
         clear_error();
         return 0;
     }
@@ -40,9 +40,10 @@ int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, Rec
 }
 
 size_t rec_workspace_bytes(int batch, int hidden) {
-    // Two exchange slots of [B, 3H] words (the backward's size; the forward
-    // uses [B, H]) followed by the abort flag.
-    return align_up((size_t)2 * batch * 3 * hidden * sizeof(unsigned long long), 256) + 256;
+    // Two exchange slots of [B, 4H] words followed by the abort flag.  The
+    // largest users: the tiled backward ([B, 3H] gate gradients) and the
+    // register backward ([B, S, H] partial sums, S = ceil(H/64) <= 4).
+    return align_up((size_t)2 * batch * 4 * hidden * sizeof(unsigned long long), 256) + 256;
 }
 
 namespace {
@@ -74,6 +75,24 @@ int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, hipStream_t stream)
 }
 
 }  // namespace
+
+namespace {
+__global__ void eval_gate_kernel(const float* __restrict__ x, float* __restrict__ sig, float* __restrict__ th, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        sig[i] = rec::sigmoid_f(x[i]);
+        th[i] = rec::tanh_f(x[i]);
+    }
+}
+}  // namespace
+
+int eval_gate_functions(const float* x, float* sig, float* th, int n, hipStream_t stream) {
+    if (n < 0 || (n > 0 && (!x || !sig || !th))) return fail(RKA_ERR_INVALID_ARGUMENT, "eval_gate_functions: bad args");
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(eval_gate_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, sig, th, n);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
 
 int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
                        float* y, float* hn, float* reserve, void* ws, size_t ws_bytes,

@@ -302,8 +302,8 @@ int rka_set_recurrence_config(int dir, int kind, int units, int param) {
         if (!(units == 0 || (units > 0 && units <= 64 && (64 % units) == 0)) || !ok_p)
             return fail(RKA_ERR_INVALID_ARGUMENT, "tiled: units must divide 64, pair_waves be 1, 2 or 4 (0 = auto)");
     } else if (kind == REC_REGISTER) {
-        if (!ok_p) return fail(RKA_ERR_INVALID_ARGUMENT, "register: rows must be 1, 2 or 4 (0 = auto)");
-        units = 0;
+        if (!ok_p || !(units == 0 || units == 64))
+            return fail(RKA_ERR_INVALID_ARGUMENT, "register: units 64 (or 0), rows 1, 2 or 4 (0 = auto)");
     } else {
         return fail(RKA_ERR_INVALID_ARGUMENT, "kind must be 0 (auto), 1 (tiled) or 2 (register)");
     }
@@ -322,6 +322,13 @@ int rka_describe_recurrence(int dir, int batch, int hidden_size, int out8[8]) {
     const int v[8] = {c.kind, c.groups, c.slices, c.units, c.rows, c.pair_waves, c.chunk, c.lds_bytes};
     for (int i = 0; i < 8; ++i) out8[i] = v[i];
     return 0;
+}
+
+int rka_eval_gate_functions(const float* x, float* sigmoid_out, float* tanh_out, int n, void* stream) {
+    clear_error();
+    const DeviceInfo* dev = nullptr;
+    RKA_RETURN_IF_ERR(current_device_info(&dev));
+    return eval_gate_functions(x, sigmoid_out, tanh_out, n, reinterpret_cast<hipStream_t>(stream));
 }
 
 int rka_profile_enable(int on) {

@@ -92,6 +92,7 @@ int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, Rec
 void set_rec_override(int dir, int kind, int units, int param);
 
 size_t rec_workspace_bytes(int batch, int hidden);
+int eval_gate_functions(const float* x, float* sig, float* th, int n, hipStream_t stream);
 
 int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
                        float* y, float* hn, float* reserve, void* ws, size_t ws_bytes,

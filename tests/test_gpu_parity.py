@@ -78,6 +78,32 @@ def test_gemm_unaligned_operands_use_scalar_path(gpu, hip_lib):
     assert (c[:, :n].double().cpu() - ref).abs().max().item() < 1e-4
 
 
+# ------------------------------------------------- gate nonlinearities ---
+def test_gate_functions_accuracy_against_float64(gpu, hip_lib):
+    """The recurrence kernels evaluate sigmoid / tanh from their definitions on
+    the hardware exp2 / rcp units; bound their error over the range that
+    matters (saturated tails included) against float64."""
+    from rnn_kernel_amd import _lib
+
+    x = torch.cat([torch.linspace(-30, 30, 200001), torch.tensor([0.0, -0.0, 1e-30, -1e-30, 1e-6, -1e-6, 88.0,
+                                                                  -88.0, 200.0, -200.0, float("inf"), float("-inf")])])
+    xd = x.to(gpu)
+    sig = torch.empty_like(xd)
+    th = torch.empty_like(xd)
+    rc = hip_lib.rka_eval_gate_functions(xd.data_ptr(), sig.data_ptr(), th.data_ptr(), x.numel(),
+                                         torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "rka_eval_gate_functions")
+    torch.cuda.synchronize()
+    x64 = x.double()
+    ref_sig = torch.sigmoid(x64)
+    ref_th = torch.tanh(x64)
+    err_sig = (sig.double().cpu() - ref_sig).abs().max().item()
+    err_th = (th.double().cpu() - ref_th).abs().max().item()
+    print(f"gate functions: max abs err sigmoid {err_sig:.3e} tanh {err_th:.3e}", flush=True)
+    assert err_sig <= 2.5e-7 and err_th <= 5e-7
+    assert torch.all((sig >= 0) & (sig <= 1)) and torch.all((th >= -1) & (th <= 1))
+
+
 # ------------------------------------------- single layer vs the oracle ---
 LAYER_SHAPES = [
     # B, T, I, H
