@@ -51,6 +51,33 @@ def stage_flops(B, T, I, H):
     }
 
 
+def stage_bytes(B, T, I, H):
+    """Algorithmic HBM bytes per launch of the recurrence kernels: every input
+    read once, every output written once (fp32)."""
+    return {
+        # gx, W_hh, b_hh, h0 in; y, reserve (r, z, n, W_hn h + b_hn), hn out
+        "forward_recurrence": 4.0 * (B * T * 3 * H + 3 * H * H + 3 * H + B * H + B * T * H + B * T * 4 * H + B * H),
+        # dy, reserve, y (h_{t-1}), W_hh, h0 in; G = (da_n, dr, dz, dn), dh0 out
+        "backward_recurrence": 4.0 * (B * T * H + B * T * 4 * H + B * T * H + 3 * H * H + B * H + B * T * 4 * H + B * H),
+    }
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gru_c2_recurrence_hbm_traffic.txt")
+
+
+def measured_traffic(stage):
+    """HBM bytes per launch of `stage` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-calibrated), or None if it has no such line."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == stage:
+                return int(f[2])
+    except OSError:
+        pass
+    return None
+
+
 def make_inputs():
     import torch
 
@@ -122,7 +149,8 @@ def torch_cpu_baseline(budget_s: float):
     import torch
     import torch.nn.functional as F
 
-    threads = os.cpu_count() or 1
+    # the GPU box's CPU share is 16 threads whatever os.cpu_count() reports
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")))
     torch.set_num_threads(threads)
     gru, x, h0, target = make_inputs()
     t_sample = 16
@@ -183,6 +211,7 @@ def main():
     dominant = max(stage_avg, key=stage_avg.get)
     dom_ms = stage_avg[dominant]
     achieved = flops[dominant] / (dom_ms * 1e-3) / 1e12 if dom_ms > 0 else 0.0
+    alg_bytes = stage_bytes(B, T, I, H).get(dominant)
 
     result = {
         "metric": METRIC,
@@ -210,9 +239,14 @@ def main():
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
-            "traffic": None,
-            "note": "serial recurrence: latency-bound; achieved = algorithmic FLOPs / measured duration",
+            "traffic": measured_traffic(dominant),
+            "note": ("serial recurrence, latency-bound (one cross-workgroup exchange per timestep); achieved = "
+                     "algorithmic FLOPs / mean launch time from hipEvents on the launch stream; traffic = "
+                     "copy-calibrated FETCH_SIZE+WRITE_SIZE bytes per launch from the committed rocprofv3 summary"),
             "us_per_timestep": dom_ms * 1e3 / T,
+            "launch_ms": dom_ms,
+            "alg_bytes": alg_bytes,
+            "hbm_frac": (alg_bytes / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS) if (alg_bytes and dom_ms > 0) else None,
         },
     }
 
