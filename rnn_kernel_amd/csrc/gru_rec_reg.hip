@@ -8,18 +8,29 @@
 //   backward: wavefront w holds, per lane, the j-chunk of its unit's column
 //             of W_hh over the 3H gate rows (chunk registers).
 // Each step a wavefront polls only the exchanged words of its own chunk
-// (h_{t-1} forward, G_h,t backward; one word per lane), broadcasts them with
-// readlane into scalar operands and runs the chunk's FMAs without touching
-// LDS; the 8 wavefront partials are reduced in LDS (one barrier per step) and
-// wavefront r applies the gate math of row r.  With 64 units per workgroup a
-// hidden size of 256 needs 4 exchanging workgroups per batch row, which sit
-// on one XCD.
+// (h_{t-1} forward, G_h,t backward; one word per lane per 64), turns them
+// into groups of 16 values replicated in the four 16-lane rows
+// (v_permlane16/32_swap) and runs the chunk's FMAs with the broadcast folded
+// into each FMA (DPP row_newbcast), without LDS or readlane; the 8 wavefront
+// partials are reduced in LDS (one barrier per step) and wavefront r applies
+// the gate math of row r.  With 64 units per workgroup a hidden size of 256
+// needs 4 exchanging workgroups per batch row, which sit on one XCD.
 //
-// Alternatives measured slower on MI355X at B=64, H=256, T=512 (kept out):
+// Measured on MI355X at B=64, H=256, T=512 (same box, alternating runs):
+//   * readlane broadcasts into scalar FMA operands instead of DPP: forward
+//     0.726 vs 0.706 ms, backward 1.182 vs 0.934 ms (a readlane costs ~11
+//     cycles of issue per wave, a DPP FMA ~5-7, a plain FMA ~5-6);
+//   * polling 16-word groups replicated in every row (6 loads per backward
+//     wave) instead of one word per lane: backward 1.25 vs 0.95 ms;
+//   * exec-masking lanes without a word instead of letting them re-read a
+//     word of their own wave: backward 1.04 vs 0.93 ms.
+// Alternatives measured slower earlier (kept out):
 //   * 128 units per workgroup (2 exchanging workgroups, but twice the FMAs on
 //     the owner's critical path): forward 1.67 vs 1.29 us/step;
 //   * a ninth, non-polling wavefront for the gate math (it shares a SIMD with
 //     two polling wavefronts): forward 1.6 vs 1.29 us/step;
+//   * a poller wavefront relaying the exchanged words through LDS to the
+//     others: forward 2.48 vs 1.54 us/step, backward 3.16 vs 2.21 us/step;
 //   * backward exchanging per-slice partial sums of dh (forward-sized
 //     exchange, one polling wavefront, but a second barrier and the FMAs
 //     ahead of the publish): 2.56 vs ~2.3 us/step.
@@ -47,6 +58,38 @@ struct RegParams {
     int chunk;     // k (forward) or j (backward) values per wavefront
     int wvec;      // forward: W_hh rows may be read as aligned float4
 };
+
+// Row-broadcast dot products over one group of 16 values.  A VGPR operand
+// of a DPP instruction (the accumulator of v_fmac_f32 is one) written by a
+// preceding VALU instruction needs wait states before it is read (the
+// compiler pads with s_nop below a distance of about five), so consecutive
+// FMAs go to independent partial sums: K parity for the three gates of the
+// forward (distance 6), K mod 8 for the backward (distance 8).
+//   a?[K & 1][r] += src[r](lane K of the row) * w?[K], K = 0..15
+template <int ROWS, int K = 0>
+__device__ __forceinline__ void dot16x3(float (&ar)[2][ROWS], float (&az)[2][ROWS], float (&an)[2][ROWS],
+                                        const float (&src)[ROWS], const float* wr, const float* wz,
+                                        const float* wn) {
+    if constexpr (K < 16) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            rec::fma_row_bcast<K>(ar[K & 1][r], src[r], wr[K]);
+            rec::fma_row_bcast<K>(az[K & 1][r], src[r], wz[K]);
+            rec::fma_row_bcast<K>(an[K & 1][r], src[r], wn[K]);
+        }
+        dot16x3<ROWS, K + 1>(ar, az, an, src, wr, wz, wn);
+    }
+}
+
+//   acc[K & 7][r] += src[r](lane K of the row) * w[K], K = 0..15
+template <int ROWS, int K = 0>
+__device__ __forceinline__ void dot16(float (&acc)[8][ROWS], const float (&src)[ROWS], const float* w) {
+    if constexpr (K < 16) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) rec::fma_row_bcast<K>(acc[K & 7][r], src[r], w[K]);
+        dot16<ROWS, K + 1>(acc, src, w);
+    }
+}
 
 // ------------------------------------------------------------- forward ---
 template <int NK, int ROWS>
@@ -114,51 +157,76 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
     if (threadIdx.x == 0) s_abort = 0;
     __syncthreads();
 
-    const int kk = kbeg + lane;
-    const bool kvalid = lane < p.chunk && kk < H;
+    // Lane l polls k = kbeg + 64 q + l (NP words per lane); the 16-value
+    // groups the row-broadcast FMAs consume are then built in registers.
+    constexpr int NV = NK / 16;
+    constexpr int NP = (NK + 63) / 64;
+    bool kvalid[NP];
+    int kidx[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        const int kc = 64 * q + rec::poll_lane<NV>(q, lane);
+        kvalid[q] = kc < p.chunk && kbeg + kc < H;
+        // invalid lanes re-read the wave's last valid word (or word 0)
+        kidx[q] = kvalid[q] ? kbeg + kc : rec::last_valid(kbeg, p.chunk, H);
+    }
     bool aborted = false;
     for (int t = 0; t < T; ++t) {
         // @probe:step_begin
-        // h_{t-1}[row][kbeg + lane]
-        float hv[ROWS];
+        // h_{t-1}[row][kbeg + 64 p + lane]
+        float hx[NP][ROWS];
         if (t == 0) {
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-                hv[r] = (kvalid && row0 + r < B) ? h0[(size_t)(row0 + r) * H + kk] : 0.f;
+            for (int q = 0; q < NP; ++q)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r)
+                    hx[q][r] = (kvalid[q] && row0 + r < B) ? h0[(size_t)(row0 + r) * H + kidx[q]] : 0.f;
         } else {
             const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H;
-            unsigned long long w[ROWS];
+            constexpr int N = NP * ROWS;
+            const unsigned long long* pp[N];
+            bool pv[N];
+            unsigned long long w[N];
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-                w[r] = (kvalid && row0 + r < B) ? rec::load_word(src + (size_t)(row0 + r) * H + kk) : 0ull;
+            for (int q = 0; q < NP; ++q)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    const int e = q * ROWS + r;
+                    pv[e] = kvalid[q] && row0 + r < B;
+                    pp[e] = src + (size_t)(row0 + r < B ? row0 + r : row0) * H + kidx[q];
+                    w[e] = rec::load_word(pp[e]);
+                }
             bool ok = true;
+            rec::wait_words<N>(pp, pv, w, (unsigned)t, abort_flag, ok);
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                hv[r] = (kvalid && row0 + r < B)
-                            ? rec::wait_word(src + (size_t)(row0 + r) * H + kk, w[r], (unsigned)t, abort_flag, ok)
-                            : 0.f;
-            }
+            for (int q = 0; q < NP; ++q)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    const int e = q * ROWS + r;
+                    hx[q][r] = pv[e] ? __uint_as_float((unsigned)w[e]) : 0.f;
+                }
             if (!ok) s_abort = 1;
         }
+        float hv[NV][ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) rec::replicate_rows<NV>(hx, r, hv);
         // @probe:polled
-        float ar[ROWS], az[ROWS], an[ROWS];
+        float ar[2][ROWS], az[2][ROWS], an[2][ROWS];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) ar[r] = az[r] = an[r] = 0.f;
+        for (int e = 0; e < 2; ++e)
 #pragma unroll
-        for (int k = 0; k < NK; ++k) {
+            for (int r = 0; r < ROWS; ++r) ar[e][r] = az[e][r] = an[e][r] = 0.f;
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const float hk = rec::bcast(hv[r], k);
-                ar[r] = fmaf(hk, wr[k], ar[r]);
-                az[r] = fmaf(hk, wz[k], az[r]);
-                an[r] = fmaf(hk, wn[k], an[r]);
-            }
+        for (int v = 0; v < NV; ++v) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) rec::dpp_src_guard(hv[v][r]);
+            dot16x3<ROWS>(ar, az, an, hv[v], wr + 16 * v, wz + 16 * v, wn + 16 * v);
         }
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
-            part[t & 1][wave][0][r][lane] = ar[r];
-            part[t & 1][wave][1][r][lane] = az[r];
-            part[t & 1][wave][2][r][lane] = an[r];
+            part[t & 1][wave][0][r][lane] = ar[0][r] + ar[1][r];
+            part[t & 1][wave][1][r][lane] = az[0][r] + az[1][r];
+            part[t & 1][wave][2][r][lane] = an[0][r] + an[1][r];
         }
         // @probe:computed
         __syncthreads();
@@ -246,10 +314,17 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
     if (threadIdx.x == 0) s_abort = 0;
     __syncthreads();
 
-    const int j0 = jbeg + lane;
-    const int j1 = jbeg + 64 + lane;
-    const bool v0 = lane < p.chunk && j0 < H3;
-    const bool v1 = NJ > 64 && 64 + lane < p.chunk && j1 < H3;
+    // Lane l polls j = jbeg + 64 p + l (see the forward).
+    constexpr int NV = NJ / 16;
+    constexpr int NP = (NJ + 63) / 64;
+    bool jvalid[NP];
+    int jidx[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        const int jc = 64 * q + rec::poll_lane<NV>(q, lane);
+        jvalid[q] = jc < p.chunk && jbeg + jc < H3;
+        jidx[q] = jvalid[q] ? jbeg + jc : rec::last_valid(jbeg, p.chunk, H3);
+    }
     bool aborted = false;
     float ddirect = 0.f;
     for (int i = 0; i < T; ++i) {
@@ -287,47 +362,52 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
             }
         }
         // @probe:published
-        // G_h,t[row][jbeg + lane] and [jbeg + 64 + lane]
-        float gv0[ROWS], gv1[ROWS];
+        // G_h,t[row][j] of group v
+        float gx_[NP][ROWS];
         {
-            unsigned long long w0[ROWS], w1[ROWS];
+            constexpr int N = NP * ROWS;
+            const unsigned long long* pp[N];
+            bool pv[N];
+            unsigned long long wd[N];
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const bool rv = row0 + r < B;
-                const unsigned long long* rp = slotp + (size_t)(row0 + r) * H3;
-                w0[r] = (rv && v0) ? rec::load_word(rp + j0) : 0ull;
-                w1[r] = (rv && v1) ? rec::load_word(rp + j1) : 0ull;
-            }
-            bool ok = true;
-#pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const bool rv = row0 + r < B;
-                const unsigned long long* rp = slotp + (size_t)(row0 + r) * H3;
-                gv0[r] = (rv && v0) ? rec::wait_word(rp + j0, w0[r], tag, abort_flag, ok) : 0.f;
-                gv1[r] = (rv && v1) ? rec::wait_word(rp + j1, w1[r], tag, abort_flag, ok) : 0.f;
-            }
-            if (!ok) s_abort = 1;
-        }
-        // @probe:polled
-        float acc[ROWS];
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) acc[r] = 0.f;
-        // Blocks of 16 broadcasts keep a block's scalar operands live only
-        // while its FMAs run.
-#pragma unroll
-        for (int jb = 0; jb < NJ; jb += 16) {
-#pragma unroll
-            for (int jj = jb; jj < (jb + 16 < NJ ? jb + 16 : NJ); ++jj) {
+            for (int q = 0; q < NP; ++q)
 #pragma unroll
                 for (int r = 0; r < ROWS; ++r) {
-                    const float gk = jj < 64 ? rec::bcast(gv0[r], jj) : rec::bcast(gv1[r], jj - 64);
-                    acc[r] = fmaf(gk, w[jj], acc[r]);
+                    const int e = q * ROWS + r;
+                    pv[e] = jvalid[q] && row0 + r < B;
+                    pp[e] = slotp + (size_t)(row0 + r < B ? row0 + r : row0) * H3 + jidx[q];
+                    wd[e] = rec::load_word(pp[e]);
                 }
-            }
-            __builtin_amdgcn_sched_barrier(0);
+            bool ok = true;
+            rec::wait_words<N>(pp, pv, wd, tag, abort_flag, ok);
+#pragma unroll
+            for (int q = 0; q < NP; ++q)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    const int e = q * ROWS + r;
+                    gx_[q][r] = pv[e] ? __uint_as_float((unsigned)wd[e]) : 0.f;
+                }
+            if (!ok) s_abort = 1;
+        }
+        float gv[NV][ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) rec::replicate_rows<NV>(gx_, r, gv);
+        // @probe:polled
+        float acc[8][ROWS];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) acc[e][r] = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) rec::dpp_src_guard(gv[v][r]);
+            dot16<ROWS>(acc, gv[v], w + 16 * v);
         }
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) part[i & 1][wave][r][lane] = acc[r];
+        for (int r = 0; r < ROWS; ++r)
+            part[i & 1][wave][r][lane] =
+                ((acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r])) + ((acc[4][r] + acc[5][r]) + (acc[6][r] + acc[7][r]));
         // @probe:computed
         __syncthreads();
         // @probe:synced
@@ -346,15 +426,15 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
 }
 
 // ------------------------------------------------------------- config ---
-constexpr int kFwdNK[] = {8, 16, 24, 32};
-constexpr int kBwdNJ[] = {24, 48, 72, 96};
+// Compiled per-wavefront capacities; the row-broadcast FMAs consume the
+// chunk in groups of 16.
+constexpr int kFwdNK[] = {16, 32};
+constexpr int kBwdNJ[] = {32, 48, 64, 96};
 
 template <int ROWS>
 const void* fwd_ptr(int nk) {
     switch (nk) {
-        case 8: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<8, ROWS>);
         case 16: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<16, ROWS>);
-        case 24: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<24, ROWS>);
         default: return reinterpret_cast<const void*>(&gru_fwd_reg_kernel<32, ROWS>);
     }
 }
@@ -362,9 +442,9 @@ const void* fwd_ptr(int nk) {
 template <int ROWS>
 const void* bwd_ptr(int nj) {
     switch (nj) {
-        case 24: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<24, ROWS>);
+        case 32: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<32, ROWS>);
         case 48: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<48, ROWS>);
-        case 72: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<72, ROWS>);
+        case 64: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<64, ROWS>);
         default: return reinterpret_cast<const void*>(&gru_bwd_reg_kernel<96, ROWS>);
     }
 }
@@ -383,7 +463,7 @@ const void* kernel_ptr(int dir, int cap, int rows) {
 // Per-wavefront chunk and the smallest compiled capacity that holds it.
 void chunk_of(int dir, int H, int* chunk, int* cap) {
     const int len = dir == 0 ? H : 3 * H;
-    *chunk = (len + NW - 1) / NW;
+    *chunk = ((len + NW - 1) / NW + 15) / 16 * 16;
     *cap = 0;
     if (dir == 0) {
         for (int c : kFwdNK)
