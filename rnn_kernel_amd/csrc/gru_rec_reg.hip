@@ -23,7 +23,12 @@
 //   * polling 16-word groups replicated in every row (6 loads per backward
 //     wave) instead of one word per lane: backward 1.25 vs 0.95 ms;
 //   * exec-masking lanes without a word instead of letting them re-read a
-//     word of their own wave: backward 1.04 vs 0.93 ms.
+//     word of their own wave: backward 1.04 vs 0.93 ms;
+//   * backward owner issuing its G stores and the loads of its next inputs
+//     before the poll instead of after it (inputs loaded two steps ahead,
+//     single-round polls so that no poll load is left in flight): 0.943 vs
+//     0.848 ms; the same reordering in the forward: 0.825 vs 0.782 ms (its
+//     stores and loads are few, and it keeps the two-round pipelined poll).
 // Alternatives measured slower earlier (kept out):
 //   * 128 units per workgroup (2 exchanging workgroups, but twice the FMAs on
 //     the owner's critical path): forward 1.67 vs 1.29 us/step;
@@ -197,7 +202,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
                     w[e] = rec::load_word(pp[e]);
                 }
             bool ok = true;
-            rec::wait_words<N>(pp, pv, w, (unsigned)t, abort_flag, ok);
+            rec::wait_words<N, true>(pp, pv, w, (unsigned)t, abort_flag, ok);
 #pragma unroll
             for (int q = 0; q < NP; ++q)
 #pragma unroll
@@ -299,17 +304,30 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
 
     const int prow = row0 + wave;
     const bool owner = wave < ROWS && prow < B && uvalid;
-    float dh = 0.f, dyv = 0.f, cr = 0.f, cz = 0.f, cn = 0.f, ca = 0.f, hp = 0.f;
+    // Inputs of the pointwise step t (dy, r, z, n, a_n, h_{t-1}) live in set
+    // (T - 1 - t) & 1 and are loaded two steps ahead, right after a poll: the
+    // vector-memory counter retires in order (stores included), so loads and
+    // stores issued ahead of a poll would delay its completion.
+    float dh = 0.f;
+    float ins[2][6];
+    auto load_inputs = [&](float (&d)[6], int t) {
+        const size_t bt = (size_t)prow * T + t;
+        d[0] = dy ? dy[bt * H + u] : 0.f;
+        const float* cp = reserve + bt * 4 * H;
+        d[1] = cp[u];
+        d[2] = cp[H + u];
+        d[3] = cp[2 * H + u];
+        d[4] = cp[3 * H + u];
+        d[5] = t > 0 ? y[(bt - 1) * H + u] : h0[(size_t)prow * H + u];
+    };
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int c = 0; c < 6; ++c) ins[e][c] = 0.f;
     if (owner) {
         if (dhn) dh = dhn[(size_t)prow * H + u];
-        const size_t bt = (size_t)prow * T + (T - 1);
-        if (dy) dyv = dy[bt * H + u];
-        const float* cp = reserve + bt * 4 * H;
-        cr = cp[u];
-        cz = cp[H + u];
-        cn = cp[2 * H + u];
-        ca = cp[3 * H + u];
-        hp = (T > 1) ? y[(bt - 1) * H + u] : h0[(size_t)prow * H + u];
+        load_inputs(ins[0], T - 1);
+        if (T > 1) load_inputs(ins[1], T - 2);
     }
     if (threadIdx.x == 0) s_abort = 0;
     __syncthreads();
@@ -325,44 +343,30 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
         jvalid[q] = jc < p.chunk && jbeg + jc < H3;
         jidx[q] = jvalid[q] ? jbeg + jc : rec::last_valid(jbeg, p.chunk, H3);
     }
-    bool aborted = false;
     float ddirect = 0.f;
-    for (int i = 0; i < T; ++i) {
+    // one timestep (i-th from the end); false when the workgroup must stop
+    auto step = [&](int i, float (&cur)[6]) -> bool {
         // @probe:step_begin
         const int t = T - 1 - i;
         unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
         const unsigned tag = (unsigned)(i + 1);
+        float dan = 0.f, drh = 0.f, dzh = 0.f, dnh = 0.f;
         if (owner) {
-            const float gsum = dh + dyv;
+            const float gsum = dh + cur[0];
+            const float cr = cur[1], cz = cur[2], cn = cur[3], ca = cur[4], hp = cur[5];
             const float dz = gsum * (hp - cn);
-            const float dnh = gsum * (1.0f - cz) * (1.0f - cn * cn);
-            const float dan = dnh * cr;
-            const float drh = dnh * ca * cr * (1.0f - cr);
-            const float dzh = dz * cz * (1.0f - cz);
+            dnh = gsum * (1.0f - cz) * (1.0f - cn * cn);
+            dan = dnh * cr;
+            drh = dnh * ca * cr * (1.0f - cr);
+            dzh = dz * cz * (1.0f - cz);
             ddirect = gsum * cz;
             unsigned long long* wp = slotp + (size_t)prow * H3 + u;
             rec::store_word(wp, rec::pack_word(drh, tag));
             rec::store_word(wp + H, rec::pack_word(dzh, tag));
             rec::store_word(wp + 2 * H, rec::pack_word(dan, tag));
-            const size_t bt = (size_t)prow * T + t;
-            float* op = gout + bt * 4 * H;
-            op[u] = dan;
-            op[H + u] = drh;
-            op[2 * H + u] = dzh;
-            op[3 * H + u] = dnh;
-            if (t > 0) {
-                const size_t pbt = bt - 1;
-                dyv = dy ? dy[pbt * H + u] : 0.f;
-                const float* cp = reserve + pbt * 4 * H;
-                cr = cp[u];
-                cz = cp[H + u];
-                cn = cp[2 * H + u];
-                ca = cp[3 * H + u];
-                hp = (t > 1) ? y[(pbt - 1) * H + u] : h0[(size_t)prow * H + u];
-            }
         }
         // @probe:published
-        // G_h,t[row][j] of group v
+        // G_h,t[row][jbeg + 64 q + lane]
         float gx_[NP][ROWS];
         {
             constexpr int N = NP * ROWS;
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
                     wd[e] = rec::load_word(pp[e]);
                 }
             bool ok = true;
-            rec::wait_words<N>(pp, pv, wd, tag, abort_flag, ok);
+            rec::wait_words<N, false>(pp, pv, wd, tag, abort_flag, ok);
 #pragma unroll
             for (int q = 0; q < NP; ++q)
 #pragma unroll
@@ -388,6 +392,14 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
                     gx_[q][r] = pv[e] ? __uint_as_float((unsigned)wd[e]) : 0.f;
                 }
             if (!ok) s_abort = 1;
+        }
+        if (owner) {
+            float* op = gout + ((size_t)prow * T + t) * 4 * H;
+            op[u] = dan;
+            op[H + u] = drh;
+            op[2 * H + u] = dzh;
+            op[3 * H + u] = dnh;
+            if (t >= 2) load_inputs(cur, t - 2);
         }
         float gv[NV][ROWS];
 #pragma unroll
@@ -411,15 +423,24 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
         // @probe:computed
         __syncthreads();
         // @probe:synced
-        if (s_abort) {
-            aborted = true;
-            break;
-        }
+        if (s_abort) return false;
         if (owner) {
             const int pb = i & 1;
             dh = ddirect + rec::tree8([&](int w2) { return part[pb][w2][wave][lane]; });
         }
         // @probe:step_end
+        return true;
+    };
+    bool aborted = false;
+    for (int i = 0; i < T; i += 2) {
+        if (!step(i, ins[0])) {
+            aborted = true;
+            break;
+        }
+        if (i + 1 < T && !step(i + 1, ins[1])) {
+            aborted = true;
+            break;
+        }
     }
     // @probe:kernel_end
     if (owner) dh0[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : dh;

@@ -107,21 +107,35 @@ __device__ __forceinline__ float wait_word(const unsigned long long* p, unsigned
     return __uint_as_float((unsigned)w);
 }
 
-// Waits for N words of this lane at once: every poll round re-reads all N
-// (two rounds in flight, as in wait_word, up to 8 words), so words published
-// together cost one round trip however many there are.  w[] holds the first reads on entry
+// Waits for N words of this lane at once: every poll round re-reads all N,
+// so words published together cost one round trip however many there are.
+// PIPELINED keeps two rounds in flight (as wait_word, up to 8 words): a word
+// is seen about half a round trip sooner, but one round is still in flight
+// on return, and the in-order vector-memory counter then makes the first
+// wait on anything issued after the poll cover that round too.  w[] holds the first reads on entry
 // and the matching words on return; a word with valid[v] false counts as
 // ready.  Every p[v] is loaded unconditionally (no exec-mask branches in the
 // loop), so an invalid lane must point at a word that a valid lane of the
 // same instruction loads: the duplicate costs no request, whereas one
 // stand-in address polled by every wave of the grid would be a hot spot.
-template <int N>
+template <int N, bool PIPELINED>
 __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[N], const bool (&valid)[N],
                                            unsigned long long (&w)[N], unsigned tag, int* abort_flag, bool& ok) {
-    auto ready = [&](const unsigned long long (&x)[N]) {
+    // Without pipelining every word is waited for and tested in each round
+    // (no short-circuit): a load still pending at the exit would be waited
+    // for later, at a point where the in-order counter also covers whatever
+    // was issued after it.
+    auto ready = [&](unsigned long long (&x)[N]) {
         bool r = true;
+        if constexpr (PIPELINED && N <= 8) {
 #pragma unroll
-        for (int v = 0; v < N; ++v) r = r && (!valid[v] || (unsigned)(x[v] >> 32) == tag);
+            for (int v = 0; v < N; ++v) r = r && (!valid[v] || (unsigned)(x[v] >> 32) == tag);
+        } else {
+#pragma unroll
+            for (int v = 0; v < N; ++v) asm volatile("" : "+v"(x[v]));
+#pragma unroll
+            for (int v = 0; v < N; ++v) r &= (!valid[v] || (unsigned)(x[v] >> 32) == tag);
+        }
         return r;
     };
     if (!ok || ready(w)) return;
@@ -134,8 +148,10 @@ __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[
         return (spins & 1023) == 0 &&
                __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
     };
-    if constexpr (N > 8) {
-        // one round in flight: three register copies of many words would spill
+    if constexpr (N > 8 || !PIPELINED) {
+        // one round in flight: three register copies of many words would spill,
+        // and a load still in flight after the wait forces the next vmcnt wait
+        // (the counter retires in order) to cover everything issued after it
         for (;;) {
 #pragma unroll
             for (int v = 0; v < N; ++v) w[v] = load_word(p[v]);
