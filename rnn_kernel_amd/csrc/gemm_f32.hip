@@ -6,7 +6,8 @@
 //   weight gradients  dW  = G^T [X | Hprev]        (A k-major,  B k-major)
 // C[m,n] = sum_k A(m,k) B(n,k).  A workgroup of 4 wavefronts computes a
 // 128x128 tile; each wavefront owns a 64x64 quadrant as 2x2 MFMA 32x32
-// blocks.  Operand tiles of 16 k-steps are staged through LDS in k-major form
+// blocks.  Operand tiles of 16 (direct) or 32 (split-K) k-steps are staged
+// through LDS in k-major form
 // ([k][row], padded) so that the MFMA operand reads of a half-wave are 32
 // consecutive floats (conflict free); the next tile is prefetched into
 // registers while the current one is consumed (double-buffered LDS, one
@@ -19,7 +20,6 @@ namespace {
 
 constexpr int BM = 128;
 constexpr int BN = 128;
-constexpr int BK = 16;
 constexpr int LDSP = BM + 4;  // padded LDS row (floats); multiple of 4 for b128 stores
 constexpr int NT = 256;
 
@@ -37,20 +37,27 @@ __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, i
     return op.ptr + (size_t)k * op.ld + r;
 }
 
-// Register staging of one BMxBK operand tile (2 float4 per thread).
-// kmajor == 0: thread -> (row tid/4 + 64 i, k 4*(tid%4) .. +3)
-// kmajor == 1: thread -> (k tid/32 + 8 i, row 4*(tid%32) .. +3)
-template <bool VEC>
+// Register staging of one BMxBK operand tile (NV4 float4 per thread).
+// kmajor == 0: thread -> (row tid/KQ + (NT/KQ) i, k 4*(tid%KQ) .. +3), KQ = BK/4
+// kmajor == 1: thread -> (k tid/32 + (NT/32) i, row 4*(tid%32) .. +3)
+// Direct products (input projection, dx) stage 16 k per tile: three
+// workgroups per CU.  Split-K weight gradients stage 32: half the barriers
+// and twice the MFMA work per load round (two workgroups per CU).
+constexpr int kDirectBK = 16;
+constexpr int kSplitBK = 32;
+static_assert(BM == 128 && BN == 128 && NT == 256, "tile staging layout");
+
+template <bool VEC, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
 __device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int kend,
-                                          int r0, int k0, int tid, float4 (&v)[2]) {
+                                          int r0, int k0, int tid, float4 (&v)[NV4]) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NV4; ++i) {
         int r, k;
         if (op.kmajor == 0) {
-            r = r0 + tid / 4 + 64 * i;
-            k = k0 + 4 * (tid % 4);
+            r = r0 + tid / KQ + (NT / KQ) * i;
+            k = k0 + 4 * (tid % KQ);
         } else {
-            k = k0 + tid / 32 + 8 * i;
+            k = k0 + tid / 32 + (NT / 32) * i;
             r = r0 + 4 * (tid % 32);
         }
         if (VEC) {
@@ -72,18 +79,19 @@ __device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int k
     }
 }
 
-__device__ __forceinline__ void store_tile(int kmajor, float* lds, int tid, const float4 (&v)[2]) {
+template <int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
+__device__ __forceinline__ void store_tile(int kmajor, float* lds, int tid, const float4 (&v)[NV4]) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NV4; ++i) {
         if (kmajor == 0) {
-            const int r = tid / 4 + 64 * i;
-            const int k = 4 * (tid % 4);
+            const int r = tid / KQ + (NT / KQ) * i;
+            const int k = 4 * (tid % KQ);
             lds[(k + 0) * LDSP + r] = v[i].x;
             lds[(k + 1) * LDSP + r] = v[i].y;
             lds[(k + 2) * LDSP + r] = v[i].z;
             lds[(k + 3) * LDSP + r] = v[i].w;
         } else {
-            const int k = tid / 32 + 8 * i;
+            const int k = tid / 32 + (NT / 32) * i;
             const int r = 4 * (tid % 32);
             *reinterpret_cast<float4*>(lds + k * LDSP + r) = v[i];
         }
@@ -99,10 +107,33 @@ struct GemmArgs {
     int ldc;
     float* partial;        // split mode: [ksplit][m][n] then colsum [ksplit][m]
     int want_colsum;
+    int tiles_m, tiles;    // split mode: output tiles along m, in total
+    int ksplit;
 };
 
-template <bool AV, bool BV, bool SPLIT>
+// Split mode runs a 1-D grid of tiles * ksplit workgroups.  Workgroups are
+// dealt to the 8 XCDs round robin (XCD = id % 8); when ksplit is a multiple
+// of 8, the tiles of one k-chunk are given consecutive ids on one XCD, so
+// the chunk's operand rows are fetched into that XCD's L2 once and re-read
+// from there by the other tiles.
+__device__ __forceinline__ void split_coords(const GemmArgs& p, int& bx, int& by, int& bz) {
+    const int id = blockIdx.x;
+    int tile;
+    if (p.ksplit % 8 == 0) {
+        const int xcd = id % 8, slot = id / 8;
+        bz = xcd + 8 * (slot / p.tiles);
+        tile = slot % p.tiles;
+    } else {
+        bz = id / p.tiles;
+        tile = id % p.tiles;
+    }
+    bx = tile % p.tiles_m;
+    by = tile / p.tiles_m;
+}
+
+template <bool AV, bool BV, bool SPLIT, int BK = SPLIT ? kSplitBK : kDirectBK>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
+    constexpr int NV4 = BM * BK / (4 * NT);
     __shared__ __attribute__((aligned(16))) float As[2][BK * LDSP];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDSP];
 
@@ -110,12 +141,14 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const int m0 = blockIdx.x * BM;
-    const int n0 = blockIdx.y * BN;
-    const int kbeg = blockIdx.z * p.kchunk;
+    int bx = blockIdx.x, by = blockIdx.y, bz = 0;
+    if (SPLIT) split_coords(p, bx, by, bz);
+    const int m0 = bx * BM;
+    const int n0 = by * BN;
+    const int kbeg = bz * p.kchunk;
     const int kend = min(p.k, kbeg + p.kchunk);
     const int nkb = (kend - kbeg + BK - 1) / BK;
-    const bool colsum = SPLIT && p.want_colsum && blockIdx.y == 0;
+    const bool colsum = SPLIT && p.want_colsum && by == 0;
 
     floatx16 acc[2][2];
 #pragma unroll
@@ -126,12 +159,12 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     float cs = 0.f;
 
-    float4 ra[2], rb[2];
+    float4 ra[NV4], rb[NV4];
     if (nkb > 0) {
-        load_tile<AV>(p.a, p.m, kend, m0, kbeg, tid, ra);
-        load_tile<BV>(p.b, p.n, kend, n0, kbeg, tid, rb);
-        store_tile(p.a.kmajor, As[0], tid, ra);
-        store_tile(p.b.kmajor, Bs[0], tid, rb);
+        load_tile<AV, BK>(p.a, p.m, kend, m0, kbeg, tid, ra);
+        load_tile<BV, BK>(p.b, p.n, kend, n0, kbeg, tid, rb);
+        store_tile<BK>(p.a.kmajor, As[0], tid, ra);
+        store_tile<BK>(p.b.kmajor, Bs[0], tid, rb);
     }
     __syncthreads();
 
@@ -139,8 +172,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
         const int cur = kb & 1;
         const bool more = kb + 1 < nkb;
         if (more) {
-            load_tile<AV>(p.a, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
-            load_tile<BV>(p.b, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
+            load_tile<AV, BK>(p.a, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
+            load_tile<BV, BK>(p.b, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
         }
         const float* as = As[cur];
         const float* bs = Bs[cur];
@@ -161,8 +194,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
             acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
         }
         if (more) {
-            store_tile(p.a.kmajor, As[cur ^ 1], tid, ra);
-            store_tile(p.b.kmajor, Bs[cur ^ 1], tid, rb);
+            store_tile<BK>(p.a.kmajor, As[cur ^ 1], tid, ra);
+            store_tile<BK>(p.b.kmajor, Bs[cur ^ 1], tid, rb);
         }
         __syncthreads();
     }
@@ -181,7 +214,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
                 const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m >= p.m) continue;
                 if (SPLIT) {
-                    p.partial[((size_t)blockIdx.z * p.m + m) * p.n + n] = acc[i][j][r];
+                    p.partial[((size_t)bz * p.m + m) * p.n + n] = acc[i][j][r];
                 } else {
                     p.c[(size_t)m * p.ldc + n] = acc[i][j][r] + bias;
                 }
@@ -189,8 +222,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
         }
     }
     if (colsum && tid < BM && m0 + tid < p.m) {
-        float* cpart = p.partial + (size_t)gridDim.z * p.m * p.n;
-        cpart[(size_t)blockIdx.z * p.m + m0 + tid] = cs;
+        float* cpart = p.partial + (size_t)p.ksplit * p.m * p.n;
+        cpart[(size_t)bz * p.m + m0 + tid] = cs;
     }
 }
 
@@ -231,8 +264,12 @@ bool vec_ok(const GemmOperand& op, int rows, int k) {
 }
 
 template <bool SPLIT>
-int launch_gemm(const GemmArgs& args, int ksplit, bool av, bool bv, hipStream_t stream) {
-    dim3 grid((args.m + BM - 1) / BM, (args.n + BN - 1) / BN, ksplit);
+int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream) {
+    const int tm = (args.m + BM - 1) / BM, tn = (args.n + BN - 1) / BN;
+    args.tiles_m = tm;
+    args.tiles = tm * tn;
+    args.ksplit = ksplit;
+    const dim3 grid = SPLIT ? dim3(tm * tn * ksplit) : dim3(tm, tn);
     if (av && bv) {
         hipLaunchKernelGGL((gemm_f32_kernel<true, true, SPLIT>), grid, dim3(NT), 0, stream, args);
     } else if (av) {
@@ -259,7 +296,7 @@ int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
     args.m = m;
     args.n = n;
     args.k = k;
-    args.kchunk = (k + BK - 1) / BK * BK;
+    args.kchunk = (k + kDirectBK - 1) / kDirectBK * kDirectBK;
     args.bias = bias;
     args.c = c;
     args.ldc = ldc;
@@ -274,9 +311,10 @@ int choose_ksplit(int m, int n, int k, int num_cus) {
     const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     const int target = 2 * (num_cus > 0 ? num_cus : 256);
     int ks = (target + tiles - 1) / tiles;
-    const int max_by_k = k / (8 * BK);  // at least 8 tiles of k per split
+    const int max_by_k = k / (8 * kSplitBK);  // at least 8 tiles of k per split
     if (ks > max_by_k) ks = max_by_k;
     if (ks > 64) ks = 64;
+    if (ks >= 8) ks = ks / 8 * 8;       // whole k-chunks per XCD (split_coords)
     if (ks < 1) ks = 1;
     return ks;
 }
@@ -293,7 +331,7 @@ int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
     args.n = n;
     args.k = k;
     const int kper = (k + ksplit - 1) / ksplit;
-    args.kchunk = (kper + BK - 1) / BK * BK;
+    args.kchunk = (kper + kSplitBK - 1) / kSplitBK * kSplitBK;
     args.partial = partial;
     args.want_colsum = colsum != nullptr;
     RKA_RETURN_IF_ERR(launch_gemm<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k), stream));
