@@ -145,6 +145,21 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
  *         0 = auto);
  * kind 2: register-resident; units = 64 (or 0), param = batch rows per
  *         workgroup (1, 2, 4, 0 = auto). */
+/* Number of time chunks the backward of a layer runs in (0 = automatic,
+ * currently 1; at most 8, and never more than seq_len).  With several chunks
+ * the backward recurrence is launched once per time range, latest first,
+ * and the gradient GEMMs of each finished range run on a second stream
+ * concurrently with the next range (slower on MI355X at the benchmark
+ * shape, hence not automatic).  Affects later calls on all threads and the
+ * backward workspace size.  No counterpart in the reference (its backward is
+ * one launch, src/rnn_kernel/a100/prod/gru.py:531-580); exported for tests
+ * and tuning. */
+int rka_set_backward_chunks(int chunks);
+
+/* Chunks rka_gru_backward uses for seq_len under the current setting
+ * (-1 on bad arguments). */
+int rka_backward_chunks(int seq_len);
+
 #define RKA_REC_AUTO 0
 #define RKA_REC_TILED 1
 #define RKA_REC_REGISTER 2

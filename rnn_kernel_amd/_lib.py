@@ -33,6 +33,8 @@ SIGNATURES = {
     "rka_gru_recurrence_forward": (_I, [_P] * 7 + [_P, _SZ, _I, _I, _I, _P]),
     "rka_gru_recurrence_backward": (_I, [_P] * 8 + [_P, _SZ, _I, _I, _I, _P]),
     "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
+    "rka_set_backward_chunks": (_I, [_I]),
+    "rka_backward_chunks": (_I, [_I]),
     "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
     "rka_eval_gate_functions": (_I, [_P, _P, _P, _I, _P]),
     "rka_profile_enable": (_I, [_I]),
@@ -117,3 +119,12 @@ def describe_recurrence(direction: int, batch: int, hidden: int) -> dict:
 
 def set_recurrence_config(direction: int, kind: int = 0, units: int = 0, param: int = 0) -> None:
     check(load().rka_set_recurrence_config(direction, kind, units, param), "rka_set_recurrence_config")
+
+
+def set_backward_chunks(chunks: int) -> None:
+    """Time chunks of the backward (0 = automatic); see rka_set_backward_chunks."""
+    check(load().rka_set_backward_chunks(chunks), "rka_set_backward_chunks")
+
+
+def backward_chunks(seq_len: int) -> int:
+    return int(load().rka_backward_chunks(seq_len))

@@ -27,8 +27,18 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // Address of element (row r, k) of an operand; handles the [h0 ; y[:, :-1]]
 // row remap used as the B operand of dW_hh.
+// SEG: the products of one backward time chunk (SegMap rows); compiled
+// separately so the other products carry no remap arithmetic.
+template <bool SEG>
+__device__ __forceinline__ int seg_map(const SegMap& s, int i) {
+    if constexpr (!SEG) return i;
+    return s.len ? (i / s.len) * s.stride + s.off + i % s.len : i;
+}
+
+template <bool SEG>
 __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, int k) {
-    if (op.kmajor == 0) return op.ptr + (size_t)r * op.ld + k;
+    if (op.kmajor == 0) return op.ptr + (size_t)seg_map<SEG>(op.seg, r) * op.ld + k;
+    k = seg_map<SEG>(op.seg, k);
     if (op.shift_T > 0) {
         const int t = k % op.shift_T;
         if (t == 0) return op.shift_first + (size_t)(k / op.shift_T) * op.ld + r;
@@ -47,7 +57,7 @@ constexpr int kDirectBK = 16;
 constexpr int kSplitBK = 32;
 static_assert(BM == 128 && BN == 128 && NT == 256, "tile staging layout");
 
-template <bool VEC, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
+template <bool VEC, bool SEG, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
 __device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int kend,
                                           int r0, int k0, int tid, float4 (&v)[NV4]) {
 #pragma unroll
@@ -64,7 +74,7 @@ __device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int k
             // Vector path: the contiguous extent is a multiple of 4 and rows
             // are 16-byte aligned, so a float4 is entirely in or out.
             const bool in = (r < rows) && (k < kend);
-            v[i] = in ? *reinterpret_cast<const float4*>(elem_ptr(op, r, k))
+            v[i] = in ? *reinterpret_cast<const float4*>(elem_ptr<SEG>(op, r, k))
                       : make_float4(0.f, 0.f, 0.f, 0.f);
         } else {
             float e[4];
@@ -72,7 +82,7 @@ __device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int k
             for (int c = 0; c < 4; ++c) {
                 const int rr = op.kmajor == 0 ? r : r + c;
                 const int kk = op.kmajor == 0 ? k + c : k;
-                e[c] = (rr < rows && kk < kend) ? *elem_ptr(op, rr, kk) : 0.f;
+                e[c] = (rr < rows && kk < kend) ? *elem_ptr<SEG>(op, rr, kk) : 0.f;
             }
             v[i] = make_float4(e[0], e[1], e[2], e[3]);
         }
@@ -108,7 +118,9 @@ struct GemmArgs {
     float* partial;        // split mode: [ksplit][m][n] then colsum [ksplit][m]
     int want_colsum;
     int tiles_m, tiles;    // split mode: output tiles along m, in total
-    int ksplit;
+    int ksplit;            // split mode: slices of this launch
+    int z_off, ksplit_total;  // split mode: first slice, slices in the buffer
+    SegMap c_seg;          // direct mode: output row map
 };
 
 // Split mode runs a 1-D grid of tiles * ksplit workgroups.  Workgroups are
@@ -131,7 +143,7 @@ __device__ __forceinline__ void split_coords(const GemmArgs& p, int& bx, int& by
     by = tile / p.tiles_m;
 }
 
-template <bool AV, bool BV, bool SPLIT, int BK = SPLIT ? kSplitBK : kDirectBK>
+template <bool AV, bool BV, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     constexpr int NV4 = BM * BK / (4 * NT);
     __shared__ __attribute__((aligned(16))) float As[2][BK * LDSP];
@@ -161,8 +173,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
 
     float4 ra[NV4], rb[NV4];
     if (nkb > 0) {
-        load_tile<AV, BK>(p.a, p.m, kend, m0, kbeg, tid, ra);
-        load_tile<BV, BK>(p.b, p.n, kend, n0, kbeg, tid, rb);
+        load_tile<AV, SEG, BK>(p.a, p.m, kend, m0, kbeg, tid, ra);
+        load_tile<BV, SEG, BK>(p.b, p.n, kend, n0, kbeg, tid, rb);
         store_tile<BK>(p.a.kmajor, As[0], tid, ra);
         store_tile<BK>(p.b.kmajor, Bs[0], tid, rb);
     }
@@ -172,8 +184,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
         const int cur = kb & 1;
         const bool more = kb + 1 < nkb;
         if (more) {
-            load_tile<AV, BK>(p.a, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
-            load_tile<BV, BK>(p.b, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
+            load_tile<AV, SEG, BK>(p.a, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
+            load_tile<BV, SEG, BK>(p.b, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
         }
         const float* as = As[cur];
         const float* bs = Bs[cur];
@@ -214,16 +226,16 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
                 const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m >= p.m) continue;
                 if (SPLIT) {
-                    p.partial[((size_t)bz * p.m + m) * p.n + n] = acc[i][j][r];
+                    p.partial[((size_t)(p.z_off + bz) * p.m + m) * p.n + n] = acc[i][j][r];
                 } else {
-                    p.c[(size_t)m * p.ldc + n] = acc[i][j][r] + bias;
+                    p.c[(size_t)seg_map<SEG>(p.c_seg, m) * p.ldc + n] = acc[i][j][r] + bias;
                 }
             }
         }
     }
     if (colsum && tid < BM && m0 + tid < p.m) {
-        float* cpart = p.partial + (size_t)p.ksplit * p.m * p.n;
-        cpart[(size_t)bz * p.m + m0 + tid] = cs;
+        float* cpart = p.partial + (size_t)p.ksplit_total * p.m * p.n;
+        cpart[(size_t)(p.z_off + bz) * p.m + m0 + tid] = cs;
     }
 }
 
@@ -263,30 +275,41 @@ bool vec_ok(const GemmOperand& op, int rows, int k) {
     return true;
 }
 
+template <bool SPLIT, bool SEG>
+int launch_gemm_t(const GemmArgs& args, dim3 grid, bool av, bool bv, hipStream_t stream) {
+    if (av && bv) {
+        hipLaunchKernelGGL((gemm_f32_kernel<true, true, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
+    } else if (av) {
+        hipLaunchKernelGGL((gemm_f32_kernel<true, false, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
+    } else if (bv) {
+        hipLaunchKernelGGL((gemm_f32_kernel<false, true, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL((gemm_f32_kernel<false, false, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
+    }
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
 template <bool SPLIT>
 int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream) {
     const int tm = (args.m + BM - 1) / BM, tn = (args.n + BN - 1) / BN;
     args.tiles_m = tm;
     args.tiles = tm * tn;
     args.ksplit = ksplit;
-    const dim3 grid = SPLIT ? dim3(tm * tn * ksplit) : dim3(tm, tn);
-    if (av && bv) {
-        hipLaunchKernelGGL((gemm_f32_kernel<true, true, SPLIT>), grid, dim3(NT), 0, stream, args);
-    } else if (av) {
-        hipLaunchKernelGGL((gemm_f32_kernel<true, false, SPLIT>), grid, dim3(NT), 0, stream, args);
-    } else if (bv) {
-        hipLaunchKernelGGL((gemm_f32_kernel<false, true, SPLIT>), grid, dim3(NT), 0, stream, args);
-    } else {
-        hipLaunchKernelGGL((gemm_f32_kernel<false, false, SPLIT>), grid, dim3(NT), 0, stream, args);
+    if (!SPLIT) {
+        args.z_off = 0;
+        args.ksplit_total = 1;
     }
-    RKA_RETURN_IF_HIP(hipGetLastError());
-    return 0;
+    const dim3 grid = SPLIT ? dim3(tm * tn * ksplit) : dim3(tm, tn);
+    const bool seg = args.a.seg.len || args.b.seg.len || args.c_seg.len;
+    return seg ? launch_gemm_t<SPLIT, true>(args, grid, av, bv, stream)
+               : launch_gemm_t<SPLIT, false>(args, grid, av, bv, stream);
 }
 
 }  // namespace
 
 int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
-                const float* bias, float* c, int ldc, hipStream_t stream) {
+                const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg) {
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
     if (!a.ptr || !b.ptr || !c) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: null operand");
     if (m > 65535 * BM || n > 65535 * BN) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
@@ -300,6 +323,7 @@ int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
     args.bias = bias;
     args.c = c;
     args.ldc = ldc;
+    args.c_seg = c_seg;
     return launch_gemm<false>(args, 1, vec_ok(a, m, k), vec_ok(b, n, k), stream);
 }
 
@@ -307,9 +331,9 @@ size_t splitk_partial_floats(int m, int n, int ksplit) {
     return (size_t)ksplit * m * n + (size_t)ksplit * m;
 }
 
-int choose_ksplit(int m, int n, int k, int num_cus) {
+int choose_ksplit(int m, int n, int k, int num_cus, int wgs_per_cu) {
     const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-    const int target = 2 * (num_cus > 0 ? num_cus : 256);
+    const int target = wgs_per_cu > 0 ? wgs_per_cu * (num_cus > 0 ? num_cus : 256) : (num_cus > 0 ? num_cus : 256) / 2;
     int ks = (target + tiles - 1) / tiles;
     const int max_by_k = k / (8 * kSplitBK);  // at least 8 tiles of k per split
     if (ks > max_by_k) ks = max_by_k;
@@ -319,11 +343,11 @@ int choose_ksplit(int m, int n, int k, int num_cus) {
     return ks;
 }
 
-int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
-                float* c, int ldc, float* colsum, int rot,
-                float* partial, int ksplit, hipStream_t stream) {
+int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum,
+                         float* partial, int ksplit, int z_off, int ksplit_total, hipStream_t stream) {
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
-    if (ksplit < 1) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: ksplit must be >= 1");
+    if (ksplit < 1 || z_off < 0 || z_off + ksplit > ksplit_total)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: bad split slices");
     GemmArgs args{};
     args.a = a;
     args.b = b;
@@ -333,14 +357,27 @@ int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
     const int kper = (k + ksplit - 1) / ksplit;
     args.kchunk = (kper + kSplitBK - 1) / kSplitBK * kSplitBK;
     args.partial = partial;
-    args.want_colsum = colsum != nullptr;
-    RKA_RETURN_IF_ERR(launch_gemm<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k), stream));
+    args.want_colsum = want_colsum ? 1 : 0;
+    args.z_off = z_off;
+    args.ksplit_total = ksplit_total;
+    return launch_gemm<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k), stream);
+}
+
+int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,
+                  float* colsum, hipStream_t stream) {
     const size_t total = (size_t)m * n + (colsum ? m : 0);
     const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, ksplit, m, n, rot,
-                       c, ldc, colsum);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, ksplit_total, m, n,
+                       rot, c, ldc, colsum);
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
+}
+
+int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
+                float* c, int ldc, float* colsum, int rot,
+                float* partial, int ksplit, hipStream_t stream) {
+    RKA_RETURN_IF_ERR(gemm_splitk_partials(m, n, k, a, b, colsum != nullptr, partial, ksplit, 0, ksplit, stream));
+    return splitk_reduce(m, n, partial, ksplit, rot, c, ldc, colsum, stream);
 }
 
 }  // namespace rka

@@ -62,6 +62,7 @@ struct RegParams {
     int G, S;      // groups of ROWS rows, slices of 64 units
     int chunk;     // k (forward) or j (backward) values per wavefront
     int wvec;      // forward: W_hh rows may be read as aligned float4
+    int t_begin, t_end;  // backward: time range processed
 };
 
 // Row-broadcast dot products over one group of 16 values.  A VGPR operand
@@ -324,10 +325,12 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
     for (int e = 0; e < 2; ++e)
 #pragma unroll
         for (int c = 0; c < 6; ++c) ins[e][c] = 0.f;
+    // steps i0 .. i1-1 (i = T-1-t) of the time range
+    const int i0 = T - p.t_end, i1 = T - p.t_begin;
     if (owner) {
         if (dhn) dh = dhn[(size_t)prow * H + u];
-        load_inputs(ins[0], T - 1);
-        if (T > 1) load_inputs(ins[1], T - 2);
+        load_inputs(ins[0], T - 1 - i0);
+        if (i0 + 1 < i1) load_inputs(ins[1], T - 2 - i0);
     }
     if (threadIdx.x == 0) s_abort = 0;
     __syncthreads();
@@ -399,7 +402,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
             op[H + u] = drh;
             op[2 * H + u] = dzh;
             op[3 * H + u] = dnh;
-            if (t >= 2) load_inputs(cur, t - 2);
+            if (t - 2 >= p.t_begin) load_inputs(cur, t - 2);
         }
         float gv[NV][ROWS];
 #pragma unroll
@@ -432,12 +435,12 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
         return true;
     };
     bool aborted = false;
-    for (int i = 0; i < T; i += 2) {
+    for (int i = i0; i < i1; i += 2) {
         if (!step(i, ins[0])) {
             aborted = true;
             break;
         }
-        if (i + 1 < T && !step(i + 1, ins[1])) {
+        if (i + 1 < i1 && !step(i + 1, ins[1])) {
             aborted = true;
             break;
         }
@@ -533,7 +536,7 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     if (cap == 0 || chunk != c.chunk) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: bad config");
     const bool aligned = (reinterpret_cast<uintptr_t>(a.w_hh) & 15u) == 0;
     RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
-                  (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0};
+                  (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end};
     const void* k = kernel_ptr(dir, cap, c.rows);
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,

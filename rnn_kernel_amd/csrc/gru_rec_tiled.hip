@@ -32,6 +32,7 @@ struct RecParams {
     int RP;            // padded LDS row length (floats) of the exchanged rows
     int KCH;           // k-chunk per wavefront (multiple of 4)
     int KLEN;          // dot-product length rounded up to 4 (H fwd, 3H bwd)
+    int t_begin, t_end;  // backward: time range processed
 };
 
 // Gathers `nrows` rows of `len` published words with step tag `tag` from
@@ -260,11 +261,12 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     float dyv = 0.f, cr = 0.f, cz = 0.f, cn = 0.f, ca = 0.f, hp = 0.f;
     if (owner) {
         if (dhn) dh = dhn[(size_t)b * H + u];
-        const size_t bt = (size_t)b * T + (T - 1);
+        const int tl = p.t_end - 1;
+        const size_t bt = (size_t)b * T + tl;
         if (dy) dyv = dy[bt * H + u];
         const float* cp = reserve + bt * 4 * H;
         cr = cp[u]; cz = cp[H + u]; cn = cp[2 * H + u]; ca = cp[3 * H + u];
-        hp = (T > 1) ? y[(bt - 1) * H + u] : h0[(size_t)b * H + u];
+        hp = (tl > 0) ? y[(bt - 1) * H + u] : h0[(size_t)b * H + u];
     }
     const int kbeg = kc * p.KCH;
     const int kend = min(p.KLEN, kbeg + p.KCH);
@@ -274,7 +276,9 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     float ddirect = 0.f;
     __syncthreads();
 
-    for (int i = 0; i < T; ++i) {
+    // global step i = T-1-t over the time range (tags and slots continue
+    // across consecutive range launches)
+    for (int i = T - p.t_end; i < T - p.t_begin; ++i) {
         const int t = T - 1 - i;
         unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
         if (owner) {
@@ -296,7 +300,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
             op[H + u] = drh;
             op[2 * H + u] = dzh;
             op[3 * H + u] = dnh;
-            if (t > 0) {
+            if (t > p.t_begin) {
                 const size_t pbt = bt - 1;
                 dyv = dy ? dy[pbt * H + u] : 0.f;
                 const float* cp = reserve + pbt * 4 * H;
@@ -385,6 +389,8 @@ RecParams make_params(int dir, int B, int T, int H, const RecConfig& c) {
     p.KLEN = (len + 3) / 4 * 4;
     const int KC = rec::NW / c.pair_waves;
     p.KCH = ((p.KLEN + KC - 1) / KC + 3) / 4 * 4;
+    p.t_begin = 0;
+    p.t_end = T;
     return p;
 }
 
@@ -443,6 +449,8 @@ int tiled_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixe
 
 int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stream) {
     RecParams prm = make_params(dir, a.B, a.T, a.H, c);
+    prm.t_begin = a.t_begin;
+    prm.t_end = a.t_end;
     const void* k = kernel_ptr(dir, c.pair_waves);
     if (c.lds_bytes > 65536) {
         RKA_RETURN_IF_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes));

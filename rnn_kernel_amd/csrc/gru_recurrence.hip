@@ -53,7 +53,7 @@ __global__ void fill_u64_kernel(unsigned long long* __restrict__ p, size_t n) {
         p[i] = 0ull;
 }
 
-int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, hipStream_t stream) {
+int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipStream_t stream) {
     const DeviceInfo* dev = nullptr;
     RKA_RETURN_IF_ERR(current_device_info(&dev));
     RecConfig c{};
@@ -63,11 +63,14 @@ int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, hipStream_t stream)
         return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "recurrence workspace too small: need " + std::to_string(need) +
                                                      " bytes, got " + std::to_string(ws_bytes));
     // Tags start at 1, so zeroed slots never match; a fill kernel (not a
-    // memset node) keeps the sequence capturable in a HIP graph.
-    const size_t zero_words = need / sizeof(unsigned long long);
-    hipLaunchKernelGGL(fill_u64_kernel, dim3(std::min<size_t>((zero_words + 255) / 256, 1024)), dim3(256), 0,
-                       stream, reinterpret_cast<unsigned long long*>(ws), zero_words);
-    RKA_RETURN_IF_HIP(hipGetLastError());
+    // memset node) keeps the sequence capturable in a HIP graph.  A range
+    // launch that continues the previous one keeps its slots (tags grow).
+    if (zero_ws) {
+        const size_t zero_words = need / sizeof(unsigned long long);
+        hipLaunchKernelGGL(fill_u64_kernel, dim3(std::min<size_t>((zero_words + 255) / 256, 1024)), dim3(256), 0,
+                           stream, reinterpret_cast<unsigned long long*>(ws), zero_words);
+        RKA_RETURN_IF_HIP(hipGetLastError());
+    }
     a.exch = reinterpret_cast<unsigned long long*>(ws);
     a.abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + need - 256);
     if (c.kind == REC_REGISTER) return reg_launch(dir, c, a, stream);
@@ -108,13 +111,27 @@ int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, cons
     a.B = B;
     a.T = T;
     a.H = H;
-    return launch(0, a, ws, ws_bytes, stream);
+    a.t_begin = 0;
+    a.t_end = T;
+    return launch(0, a, ws, ws_bytes, true, stream);
 }
 
 int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,
                         const float* h0, const float* y, const float* w_hh,
                         float* g, float* dh0, void* ws, size_t ws_bytes,
                         int B, int T, int H, hipStream_t stream) {
+    return launch_rec_backward_range(dy, dhn, reserve, h0, y, w_hh, g, dh0, ws, ws_bytes, B, T, H, 0, T, true,
+                                     stream);
+}
+
+int launch_rec_backward_range(const float* dy, const float* dh_in, const float* reserve,
+                              const float* h0, const float* y, const float* w_hh,
+                              float* g, float* dh_out, void* ws, size_t ws_bytes,
+                              int B, int T, int H, int t_begin, int t_end, bool zero_ws, hipStream_t stream) {
+    if (t_begin < 0 || t_end > T || t_begin >= t_end)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "backward recurrence: bad time range");
+    const float* dhn = dh_in;
+    float* dh0 = dh_out;
     rec::Args a;
     a.dy = dy;
     a.dhn = dhn;
@@ -127,7 +144,9 @@ int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,
     a.B = B;
     a.T = T;
     a.H = H;
-    return launch(1, a, ws, ws_bytes, stream);
+    a.t_begin = t_begin;
+    a.t_end = t_end;
+    return launch(1, a, ws, ws_bytes, zero_ws, stream);
 }
 
 }  // namespace rka

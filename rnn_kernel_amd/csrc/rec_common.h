@@ -38,6 +38,10 @@ struct Args {
     unsigned long long* exch = nullptr;
     int* abort_flag = nullptr;
     int B = 0, T = 0, H = 0;
+    // backward: steps t_end-1 down to t_begin of a sequence of T (strides and
+    // exchange tags use the global step, so consecutive ranges continue one
+    // another on the same, once-zeroed workspace)
+    int t_begin = 0, t_end = 0;
 };
 
 // Gate nonlinearities from their definitions, on the hardware transcendental

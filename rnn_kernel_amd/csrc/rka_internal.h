@@ -48,6 +48,14 @@ int current_device_info(const DeviceInfo** out);
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // ----------------------------------------------------------------- GEMM ---
+// Segment map of a row index i of the underlying 2-D array:
+// len == 0: i; else (i / len) * stride + off + i % len.  With len = L,
+// stride = T, off = t0 it selects rows (b, t0 .. t0+L-1) of a [B, T, .]
+// tensor, i.e. one time chunk of every sequence.
+struct SegMap {
+    int len = 0, stride = 0, off = 0;
+};
+
 struct GemmOperand {
     const float* ptr = nullptr;
     int ld = 0;
@@ -58,11 +66,22 @@ struct GemmOperand {
     // [h0 ; y[:, :-1]] without materialising them.
     int shift_T = 0;
     const float* shift_first = nullptr;
+    // applied first to the underlying row (k if kmajor, else r)
+    SegMap seg{};
 };
 
-// C[m,n] = sum_k A(m,k) B(n,k) + bias[n]; direct store.
+// C[m,n] = sum_k A(m,k) B(n,k) + bias[n]; direct store (row m of C at
+// c_seg(m)).
 int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
-                const float* bias, float* c, int ldc, hipStream_t stream);
+                const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg = SegMap{});
+
+// Split-K partial products only: slices [z_off, z_off + ksplit) of a
+// partial buffer holding ksplit_total slices (layout as gemm_splitk).
+int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum,
+                         float* partial, int ksplit, int z_off, int ksplit_total, hipStream_t stream);
+// out[o] = sum of the ksplit_total slices at row (o + rot) % m; colsum likewise.
+int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,
+                  float* colsum, hipStream_t stream);
 
 // Split-K product with deterministic reduction.  Output rows are rotated:
 // out[o] = C[(o + rot) % m] (rot = 0: no rotation).  colsum (nullable)
@@ -72,7 +91,10 @@ int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
                 float* c, int ldc, float* colsum, int rot,
                 float* partial, int ksplit, hipStream_t stream);
 size_t splitk_partial_floats(int m, int n, int ksplit);
-int choose_ksplit(int m, int n, int k, int num_cus);
+// Slices for a split-K product of about wgs_per_cu workgroups per CU
+// (0: half a workgroup per CU, for products that share the GPU with a
+// concurrently running recurrence); a multiple of 8 from 8 up.
+int choose_ksplit(int m, int n, int k, int num_cus, int wgs_per_cu);
 
 // ----------------------------------------------------------- recurrence ---
 enum RecKind { REC_AUTO = 0, REC_TILED = 1, REC_REGISTER = 2 };
@@ -101,5 +123,12 @@ int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,
                         const float* h0, const float* y, const float* w_hh,
                         float* g, float* dh0, void* ws, size_t ws_bytes,
                         int B, int T, int H, hipStream_t stream);
+// Steps t_end-1 .. t_begin only: dh_in seeds dh_{t_end-1} (NULL = 0), dh_out
+// receives dh_{t_begin-1}.  Consecutive ranges (descending) on the same
+// workspace continue one another; zero_ws must be set on the first.
+int launch_rec_backward_range(const float* dy, const float* dh_in, const float* reserve,
+                              const float* h0, const float* y, const float* w_hh,
+                              float* g, float* dh_out, void* ws, size_t ws_bytes,
+                              int B, int T, int H, int t_begin, int t_end, bool zero_ws, hipStream_t stream);
 
 }  // namespace rka

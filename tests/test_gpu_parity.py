@@ -174,6 +174,74 @@ def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H
     assert _rel(pd["bias_hh"].grad, ref.db_hh) <= GRAD_REL
 
 
+@pytest.fixture
+def backward_chunks(hip_lib):
+    """Sets the backward's time-chunk count for one test, then restores auto."""
+    from rnn_kernel_amd import _lib
+
+    def set_chunks(n):
+        _lib.set_backward_chunks(n)
+
+    yield set_chunks
+    _lib.set_backward_chunks(0)
+
+
+@pytest.mark.parametrize("B,T,I,H,chunks", [
+    (3, 7, 5, 33, 2),      # odd lengths: chunks of 4 and 3 steps
+    (3, 7, 5, 33, 7),      # one step per chunk
+    (2, 9, 4, 130, 4),     # odd hidden size, tails
+    (5, 16, 8, 64, 8),     # the maximum chunk count
+    (4, 5, 3, 256, 3),     # register kernel at H = 256
+    (2, 3, 2, 40, 8),      # more chunks asked than steps: clamped to T
+])
+def test_chunked_backward_matches_oracle(gpu, oracle, rec_kind, backward_chunks, B, T, I, H, chunks):
+    """The backward in time chunks (recurrence per range, gradient GEMMs of a
+    finished range on a second stream) against the oracle."""
+    from rnn_kernel_amd import GRUFunction, _lib
+
+    backward_chunks(chunks)
+    print(f"chunked backward B={B} T={T} I={I} H={H} chunks={_lib.backward_chunks(T)} kind={rec_kind}", flush=True)
+    assert _lib.backward_chunks(T) == min(chunks, T)
+    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=31 * B + 7 * T + H + chunks)
+    f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
+                       p["bias_ih"].numpy(), p["bias_hh"].numpy())
+    ref = oracle.backward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(), f.y, f.cache,
+                          dy.numpy(), dhn.numpy())
+    xd = x.to(gpu).requires_grad_(True)
+    h0d = h0.to(gpu).requires_grad_(True)
+    pd = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
+    y, hn = GRUFunction.apply(xd, h0d, pd["weight_ih"], pd["weight_hh"], pd["bias_ih"], pd["bias_hh"])
+    torch.autograd.backward([y, hn], [dy.to(gpu), dhn.to(gpu)[None]])
+    torch.cuda.synchronize()
+    assert _rel(xd.grad, ref.dx) <= GRAD_REL
+    assert _rel(h0d.grad, ref.dh0) <= GRAD_REL
+    assert _rel(pd["weight_ih"].grad, ref.dw_ih) <= GRAD_REL
+    assert _rel(pd["weight_hh"].grad, ref.dw_hh) <= GRAD_REL
+    assert _rel(pd["bias_ih"].grad, ref.db_ih) <= GRAD_REL
+    assert _rel(pd["bias_hh"].grad, ref.db_hh) <= GRAD_REL
+
+
+def test_chunked_backward_without_input_gradient(gpu, oracle, backward_chunks):
+    """x without requires_grad: dx is skipped in every chunk, the weight
+    gradients are unchanged."""
+    from rnn_kernel_amd import GRUFunction
+
+    backward_chunks(3)
+    B, T, I, H = 4, 10, 6, 48
+    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=5)
+    f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
+                       p["bias_ih"].numpy(), p["bias_hh"].numpy())
+    ref = oracle.backward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(), f.y, f.cache,
+                          dy.numpy(), None)
+    pd = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
+    y, _ = GRUFunction.apply(x.to(gpu), h0.to(gpu), pd["weight_ih"], pd["weight_hh"], pd["bias_ih"], pd["bias_hh"])
+    y.backward(dy.to(gpu))
+    torch.cuda.synchronize()
+    assert _rel(pd["weight_ih"].grad, ref.dw_ih) <= GRAD_REL
+    assert _rel(pd["weight_hh"].grad, ref.dw_hh) <= GRAD_REL
+    assert _rel(pd["bias_hh"].grad, ref.db_hh) <= GRAD_REL
+
+
 def test_recurrence_reserve_layout_matches_oracle_cache(gpu, oracle, hip_lib):
     """The forward recurrence's reserve is (r, z, n, a_n) per [b, t] row."""
     from rnn_kernel_amd import _lib

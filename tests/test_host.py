@@ -61,6 +61,24 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     assert hip_lib.rka_set_recurrence_config(0, 1, 3, 0) == 1001   # units must divide 64
     assert hip_lib.rka_set_recurrence_config(1, 2, 0, 3) == 1001   # rows 1, 2 or 4
     assert hip_lib.rka_set_recurrence_config(0, 0, 0, 0) == 0
+    assert hip_lib.rka_set_backward_chunks(-1) == 1001
+    assert hip_lib.rka_set_backward_chunks(9) == 1001
+    assert hip_lib.rka_backward_chunks(0) == -1
+
+
+def test_backward_chunk_policy_without_gpu(hip_lib):
+    """Automatic: one time chunk; an override is clamped to seq_len; the
+    workspace grows by the dh carry buffers."""
+    from rnn_kernel_amd import _lib
+
+    try:
+        assert _lib.backward_chunks(512) == 1 and _lib.backward_chunks(127) == 1
+        one = hip_lib.rka_gru_backward_workspace_bytes(64, 100, 256, 256)
+        _lib.set_backward_chunks(3)
+        assert _lib.backward_chunks(2) == 2 and _lib.backward_chunks(512) == 3
+        assert hip_lib.rka_gru_backward_workspace_bytes(64, 100, 256, 256) > one
+    finally:
+        _lib.set_backward_chunks(0)
 
 
 def test_module_construction_and_validation_messages():
