@@ -60,6 +60,17 @@ static_assert(BM == 128 && BN == 128 && NT == 256, "tile staging layout");
 template <bool VEC, bool SEG, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
 __device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int kend,
                                           int r0, int k0, int tid, float4 (&v)[NV4]) {
+    if (VEC && r0 + BM <= rows && k0 + BK <= kend) {
+        // interior tile (the common case; the test is uniform): no per-lane
+        // bounds checks, so no exec-mask branches around the loads
+#pragma unroll
+        for (int i = 0; i < NV4; ++i) {
+            const int r = op.kmajor == 0 ? r0 + tid / KQ + (NT / KQ) * i : r0 + 4 * (tid % 32);
+            const int k = op.kmajor == 0 ? k0 + 4 * (tid % KQ) : k0 + tid / 32 + (NT / 32) * i;
+            v[i] = *reinterpret_cast<const float4*>(elem_ptr<SEG>(op, r, k));
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
         int r, k;
@@ -193,17 +204,28 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
 #pragma unroll
             for (int kk = 0; kk < BK; ++kk) cs += as[kk * LDSP + tid];
         }
+        // All operand fragments of the tile are read into distinct registers
+        // first: reusing one set per k-step would make every step's LDS reads
+        // wait for the previous step's MFMAs to consume their operands and
+        // leave the matrix core idle for an LDS latency each step.
+        constexpr int KS = BK / 2;
+        float fa0[KS], fa1[KS], fb0[KS], fb1[KS];
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            const int row = (kk + (lane >> 5)) * LDSP + (lane & 31);
-            const float a0 = as[row + wm * 64];
-            const float a1 = as[row + wm * 64 + 32];
-            const float b0 = bs[row + wn * 64];
-            const float b1 = bs[row + wn * 64 + 32];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        for (int q = 0; q < KS; ++q) {
+            const int row = (2 * q + (lane >> 5)) * LDSP + (lane & 31);
+            fa0[q] = as[row + wm * 64];
+            fa1[q] = as[row + wm * 64 + 32];
+            fb0[q] = bs[row + wn * 64];
+            fb1[q] = bs[row + wn * 64 + 32];
+        }
+        // keep the scheduler from sinking the reads back between the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb0[q], acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb1[q], acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[1][1], 0, 0, 0);
         }
         if (more) {
             store_tile<BK>(p.a.kmajor, As[cur ^ 1], tid, ra);
