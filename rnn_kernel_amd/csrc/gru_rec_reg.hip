@@ -63,6 +63,8 @@ struct RegParams {
     int chunk;     // k (forward) or j (backward) values per wavefront
     int wvec;      // forward: W_hh rows may be read as aligned float4
     int t_begin, t_end;  // backward: time range processed
+    unsigned long long* xcc_words;  // start-up XCD check (nullable)
+    unsigned xcc_tag;
 };
 
 // Row-broadcast dot products over one group of 16 values.  A VGPR operand
@@ -161,7 +163,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
         gxn = gp[2 * H + u];
     }
     if (threadIdx.x == 0) s_abort = 0;
-    __syncthreads();
+    __shared__ int s_local;
+    // the group = the S workgroups g + k G; plain publishing stores when they share an XCD
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
 
     // Lane l polls k = kbeg + 64 q + l (NP words per lane); the 16-value
     // groups the row-broadcast FMAs consume are then built in registers.
@@ -250,7 +254,8 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
             const float z = rec::sigmoid_f(gxz + sz);
             const float n = rec::tanh_f(gxn + r * sn);
             const float h = n + z * (h_prev - n);
-            rec::store_word(exch + (size_t)(t & 1) * B * H + (size_t)prow * H + u, rec::pack_word(h, (unsigned)(t + 1)));
+            rec::publish_word(exch + (size_t)(t & 1) * B * H + (size_t)prow * H + u,
+                              rec::pack_word(h, (unsigned)(t + 1)), xlocal);
             const size_t bt = (size_t)prow * T + t;
             y[bt * H + u] = h;
             if (reserve) {
@@ -333,7 +338,8 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
         if (i0 + 1 < i1) load_inputs(ins[1], T - 2 - i0);
     }
     if (threadIdx.x == 0) s_abort = 0;
-    __syncthreads();
+    __shared__ int s_local;
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
 
     // Lane l polls j = jbeg + 64 p + l (see the forward).
     constexpr int NV = NJ / 16;
@@ -364,9 +370,9 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
             dzh = dz * cz * (1.0f - cz);
             ddirect = gsum * cz;
             unsigned long long* wp = slotp + (size_t)prow * H3 + u;
-            rec::store_word(wp, rec::pack_word(drh, tag));
-            rec::store_word(wp + H, rec::pack_word(dzh, tag));
-            rec::store_word(wp + 2 * H, rec::pack_word(dan, tag));
+            rec::publish_word(wp, rec::pack_word(drh, tag), xlocal);
+            rec::publish_word(wp + H, rec::pack_word(dzh, tag), xlocal);
+            rec::publish_word(wp + 2 * H, rec::pack_word(dan, tag), xlocal);
         }
         // @probe:published
         // G_h,t[row][jbeg + 64 q + lane]
@@ -536,7 +542,8 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     if (cap == 0 || chunk != c.chunk) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: bad config");
     const bool aligned = (reinterpret_cast<uintptr_t>(a.w_hh) & 15u) == 0;
     RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
-                  (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end};
+                  (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end,
+                  a.xcc_words, a.xcc_tag};
     const void* k = kernel_ptr(dir, cap, c.rows);
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,

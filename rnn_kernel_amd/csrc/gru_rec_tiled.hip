@@ -33,6 +33,8 @@ struct RecParams {
     int KCH;           // k-chunk per wavefront (multiple of 4)
     int KLEN;          // dot-product length rounded up to 4 (H fwd, 3H bwd)
     int t_begin, t_end;  // backward: time range processed
+    unsigned long long* xcc_words;  // start-up XCD check (nullable)
+    unsigned xcc_tag;
 };
 
 // Gathers `nrows` rows of `len` published words with step tag `tag` from
@@ -145,6 +147,9 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
     const float* wr = Wl + (ul * 3) * RP;
     const float* hrow = hl + bl * RP;
     bool aborted = false;
+    __shared__ int s_local;
+    // the group = the S workgroups g + k G; plain publishing stores when they share an XCD
+    const bool xlocal = group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
     __syncthreads();
 
     for (int t = 0; t < T; ++t) {
@@ -190,7 +195,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
             const float z = sigmoid_f(gxz + sz);
             const float n = tanh_f(gxn + r * sn);
             const float h = n + z * (h_prev - n);
-            store_word(exch + (size_t)(t & 1) * B * H + (size_t)b * H + u, pack_word(h, (unsigned)(t + 1)));
+            publish_word(exch + (size_t)(t & 1) * B * H + (size_t)b * H + u, pack_word(h, (unsigned)(t + 1)), xlocal);
             const size_t bt = (size_t)b * T + t;
             y[bt * H + u] = h;
             if (reserve) {
@@ -274,6 +279,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     const float* grow = gl + bl * RP;
     bool aborted = false;
     float ddirect = 0.f;
+    __shared__ int s_local;
+    const bool xlocal = group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
     __syncthreads();
 
     // global step i = T-1-t over the time range (tags and slots continue
@@ -291,9 +298,9 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
             ddirect = gsum * cz;
             const unsigned tag = (unsigned)(i + 1);
             unsigned long long* wp = slotp + (size_t)b * H3 + u;
-            store_word(wp, pack_word(drh, tag));
-            store_word(wp + H, pack_word(dzh, tag));
-            store_word(wp + 2 * H, pack_word(dan, tag));
+            publish_word(wp, pack_word(drh, tag), xlocal);
+            publish_word(wp + H, pack_word(dzh, tag), xlocal);
+            publish_word(wp + 2 * H, pack_word(dan, tag), xlocal);
             const size_t bt = (size_t)b * T + t;
             float* op = gout + bt * 4 * H;
             op[u] = dan;
@@ -451,6 +458,8 @@ int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t st
     RecParams prm = make_params(dir, a.B, a.T, a.H, c);
     prm.t_begin = a.t_begin;
     prm.t_end = a.t_end;
+    prm.xcc_words = a.xcc_words;
+    prm.xcc_tag = a.xcc_tag;
     const void* k = kernel_ptr(dir, c.pair_waves);
     if (c.lds_bytes > 65536) {
         RKA_RETURN_IF_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes));

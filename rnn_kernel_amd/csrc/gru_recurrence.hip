@@ -39,12 +39,17 @@ int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, Rec
     return tiled_choose(dir, batch, hidden, dev, 0, 0, cfg);
 }
 
-size_t rec_workspace_bytes(int batch, int hidden) {
-    // Two exchange slots of [B, 4H] words followed by the abort flag.  The
-    // largest users: the tiled backward ([B, 3H] gate gradients) and the
-    // register backward ([B, S, H] partial sums, S = ceil(H/64) <= 4).
-    return align_up((size_t)2 * batch * 4 * hidden * sizeof(unsigned long long), 256) + 256;
+namespace {
+// Two exchange slots of [B, 4H] words (the largest user is the backward's
+// [B, 3H] gate gradients), one start-up XCD word per workgroup, then a
+// 256-byte trailer holding the abort flag.
+size_t slots_bytes(int batch, int hidden) {
+    return align_up((size_t)2 * batch * 4 * hidden * sizeof(unsigned long long), 256);
 }
+constexpr size_t kXccBytes = (size_t)rec::MAX_XCC_BLOCKS * sizeof(unsigned long long);
+}  // namespace
+
+size_t rec_workspace_bytes(int batch, int hidden) { return slots_bytes(batch, hidden) + kXccBytes + 256; }
 
 namespace {
 
@@ -73,6 +78,13 @@ int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipSt
     }
     a.exch = reinterpret_cast<unsigned long long*>(ws);
     a.abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + need - 256);
+    // Start-up XCD check words; the tag is distinct for every launch of a
+    // backward sequence continued on one workspace (its first step index + 1)
+    // and nonzero for a freshly zeroed one.
+    a.xcc_words = (size_t)c.groups * c.slices <= (size_t)rec::MAX_XCC_BLOCKS
+                      ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + slots_bytes(a.B, a.H))
+                      : nullptr;
+    a.xcc_tag = dir == 0 ? 1u : (unsigned)(a.T - a.t_end) + 1u;
     if (c.kind == REC_REGISTER) return reg_launch(dir, c, a, stream);
     return tiled_launch(dir, c, a, stream);
 }

@@ -193,6 +193,7 @@ def backward_chunks(hip_lib):
     (5, 16, 8, 64, 8),     # the maximum chunk count
     (4, 5, 3, 256, 3),     # register kernel at H = 256
     (2, 3, 2, 40, 8),      # more chunks asked than steps: clamped to T
+    (8, 9, 4, 256, 3),     # H = 256 with groups on one XCD (plain publishing stores) across ranges
 ])
 def test_chunked_backward_matches_oracle(gpu, oracle, rec_kind, backward_chunks, B, T, I, H, chunks):
     """The backward in time chunks (recurrence per range, gradient GEMMs of a
@@ -264,6 +265,48 @@ def test_recurrence_reserve_layout_matches_oracle_cache(gpu, oracle, hip_lib):
     torch.cuda.synchronize()
     assert _maxabs(res, f.cache) <= 1e-5
     assert _maxabs(y, f.y) <= 1e-5
+
+
+@pytest.mark.parametrize("B,H,local", [(64, 256, True), (8, 256, True), (4, 256, False), (3, 130, False)])
+def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H, local):
+    """Each recurrence workgroup records {XCC id, launch tag} in the workspace
+    (after the two [B, 4H] exchange slots) and publishes with plain stores
+    only when its exchange group (blocks g + k G) shares one XCD.  Workgroups
+    are dispatched to the 8 XCDs round-robin (consecutive block ids on
+    consecutive XCDs, from a starting XCD that varies by launch), so the
+    groups share an XCD exactly when the group count is a multiple of 8 (the
+    bench shape among them); the others take the agent-scope path, and both
+    give the oracle's results in the layer tests."""
+    from rnn_kernel_amd import _lib
+
+    T = 3
+    ws_bytes = hip_lib.rka_gru_recurrence_workspace_bytes(B, H)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=gpu)
+    g = torch.Generator().manual_seed(B + H)
+    gx = torch.randn(B, T, 3 * H, generator=g).to(gpu)
+    whh = (0.05 * torch.randn(3 * H, H, generator=g)).to(gpu)
+    bhh = torch.zeros(3 * H, device=gpu)
+    h0 = torch.zeros(B, H, device=gpu)
+    y = torch.empty(B, T, H, device=gpu)
+    hn = torch.empty(B, H, device=gpu)
+    rc = hip_lib.rka_gru_recurrence_forward(gx.data_ptr(), h0.data_ptr(), whh.data_ptr(), bhh.data_ptr(),
+                                            y.data_ptr(), hn.data_ptr(), None, ws.data_ptr(), ws_bytes,
+                                            B, T, H, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "rka_gru_recurrence_forward")
+    torch.cuda.synchronize()
+    assert torch.isfinite(hn).all()
+    desc = _lib.describe_recurrence(0, B, H)
+    groups, slices = desc["groups"], desc["slices"]
+    slots = (2 * B * 4 * H * 8 + 255) // 256 * 256
+    words = ws[slots:slots + 8 * groups * slices].cpu().view(torch.int64)
+    tags = (words >> 32).tolist()
+    xcc = (words & 0xFFFFFFFF).tolist()
+    assert all(t == 1 for t in tags), tags
+    assert all(0 <= x < 16 for x in xcc)
+    on_one = [len({xcc[gi + k * groups] for k in range(slices)}) == 1 for gi in range(groups)]
+    print(f"B={B} H={H} groups={groups} slices={slices} xcc of the first blocks {xcc[:16]} "
+          f"groups on one XCD: {sum(on_one)}/{groups}", flush=True)
+    assert all(on_one) == local
 
 
 # ----------------------------------- module vs torch.nn.GRU on the GPU ---
