@@ -241,10 +241,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
         // @probe:computed
         __syncthreads();
         // @probe:synced
-        if (s_abort) {
-            aborted = true;
-            break;
-        }
+        // read with the partials; the owner's step goes ahead regardless (an
+        // aborted launch only ends with NaN final states)
+        const bool abort_now = s_abort != 0;
         if (owner) {
             const int pb = t & 1;
             const float sr = bias_r + rec::tree8([&](int w2) { return part[pb][w2][0][wave][lane]; });
@@ -272,6 +271,10 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
                 gxz = gp[H + u];
                 gxn = gp[2 * H + u];
             }
+        }
+        if (abort_now) {
+            aborted = true;
+            break;
         }
         // @probe:step_end
     }
@@ -370,9 +373,10 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
             dzh = dz * cz * (1.0f - cz);
             ddirect = gsum * cz;
             unsigned long long* wp = slotp + (size_t)prow * H3 + u;
-            rec::publish_word(wp, rec::pack_word(drh, tag), xlocal);
-            rec::publish_word(wp + H, rec::pack_word(dzh, tag), xlocal);
-            rec::publish_word(wp + 2 * H, rec::pack_word(dan, tag), xlocal);
+            unsigned long long* const pp3[3] = {wp, wp + H, wp + 2 * H};
+            const unsigned long long w3[3] = {rec::pack_word(drh, tag), rec::pack_word(dzh, tag),
+                                              rec::pack_word(dan, tag)};
+            rec::publish_words<3>(pp3, w3, xlocal);
         }
         // @probe:published
         // G_h,t[row][jbeg + 64 q + lane]
@@ -432,13 +436,13 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
         // @probe:computed
         __syncthreads();
         // @probe:synced
-        if (s_abort) return false;
+        const bool abort_now = s_abort != 0;  // read with the partials
         if (owner) {
             const int pb = i & 1;
             dh = ddirect + rec::tree8([&](int w2) { return part[pb][w2][wave][lane]; });
         }
         // @probe:step_end
-        return true;
+        return !abort_now;
     };
     bool aborted = false;
     for (int i = i0; i < i1; i += 2) {

@@ -100,6 +100,25 @@ __device__ __forceinline__ void publish_word(unsigned long long* p, unsigned lon
         store_word(p, w);
 }
 
+// Publishes N words computed before the call: one branch on the (uniform)
+// locality around all N stores, and every value fixed ahead of the first
+// store.  A value computed between two stores would make the compiler wait
+// for the whole vector-memory counter (the earlier store included) before
+// it, since stores and loads retire through the same in-order counter.
+template <int N>
+__device__ __forceinline__ void publish_words(unsigned long long* const (&p)[N], const unsigned long long (&w)[N],
+                                             bool xcd_local) {
+#pragma unroll
+    for (int v = 0; v < N; ++v) asm volatile("" ::"v"(w[v]));
+    if (xcd_local) {
+#pragma unroll
+        for (int v = 0; v < N; ++v) store_word_xcd(p[v], w[v]);
+    } else {
+#pragma unroll
+        for (int v = 0; v < N; ++v) store_word(p[v], w[v]);
+    }
+}
+
 // Index of the XCD (accelerator complex die) this wavefront runs on.
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned v;
