@@ -148,19 +148,35 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
         }
     }
 
-    // gate math state of wavefront r < ROWS: row row0 + wave, unit u
-    const int prow = row0 + wave;
-    const bool owner = wave < ROWS && prow < B && uvalid;
-    float h_prev = 0.f, bias_r = 0.f, bias_z = 0.f, bias_n = 0.f, gxr = 0.f, gxz = 0.f, gxn = 0.f;
+    // Owner wavefronts (gate math of row row0 + orow, unit u): the ROWS
+    // wavefronts from the first one whose k-chunk lies in this workgroup's
+    // own slice, so the owner's poll reads words it published itself.
+    const int own0 = min(NW - 1, (64 * s) / p.chunk);
+    const int orow = (wave - own0 + NW) % NW;
+    const int prow = row0 + orow;
+    const bool owner = orow < ROWS && prow < B && uvalid;
+    float h_prev = 0.f, bias_r = 0.f, bias_z = 0.f, bias_n = 0.f;
+    // gx of step t in set t & 1, loaded one step ahead right after a poll:
+    // the vector-memory counter retires in order (stores included), so
+    // memory operations issued ahead of a poll would hold up its completion.
+    float gxs[2][3];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) gxs[e][c] = 0.f;
+    const float* gx_row = gx + (size_t)prow * T * 3 * H + u;
+    auto load_gx = [&](float (&d)[3], int t) {
+        const float* gp = gx_row + (size_t)t * 3 * H;
+        d[0] = gp[0];
+        d[1] = gp[H];
+        d[2] = gp[2 * H];
+    };
     if (owner) {
         h_prev = h0[(size_t)prow * H + u];
         bias_r = b_hh[u];
         bias_z = b_hh[H + u];
         bias_n = b_hh[2 * H + u];
-        const float* gp = gx + (size_t)prow * T * 3 * H;
-        gxr = gp[u];
-        gxz = gp[H + u];
-        gxn = gp[2 * H + u];
+        load_gx(gxs[0], 0);
     }
     if (threadIdx.x == 0) s_abort = 0;
     __shared__ int s_local;
@@ -180,8 +196,23 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
         // invalid lanes re-read the wave's last valid word (or word 0)
         kidx[q] = kvalid[q] ? kbeg + kc : rec::last_valid(kbeg, p.chunk, H);
     }
-    bool aborted = false;
-    for (int t = 0; t < T; ++t) {
+    // outputs of the previous step, stored after the next poll
+    float o_h = 0.f, o_r = 0.f, o_z = 0.f, o_n = 0.f, o_a = 0.f;
+    float* y_row = y + (size_t)prow * T * H + u;
+    float* res_row = reserve ? reserve + (size_t)prow * T * 4 * H + u : nullptr;
+    auto store_outputs = [&](int t) {
+        y_row[(size_t)t * H] = o_h;
+        if (res_row) {
+            float* cp = res_row + (size_t)t * 4 * H;
+            cp[0] = o_r;
+            cp[H] = o_z;
+            cp[2 * H] = o_n;
+            cp[3 * H] = o_a;
+        }
+    };
+    // one timestep; gate inputs in cur, next step's loaded into nxt; false
+    // when the workgroup must stop
+    auto step = [&](int t, const float (&cur)[3], float (&nxt)[3]) -> bool {
         // @probe:step_begin
         // h_{t-1}[row][kbeg + 64 p + lane]
         float hx[NP][ROWS];
@@ -220,6 +251,12 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
         float hv[NV][ROWS];
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) rec::replicate_rows<NV>(hx, r, hv);
+        // the polled words are consumed before any store or load is issued
+        // behind them (a later use would wait for those too)
+        if (owner) {
+            if (t > 0) store_outputs(t - 1);
+            if (t + 1 < T) load_gx(nxt, t + 1);
+        }
         // @probe:polled
         float ar[2][ROWS], az[2][ROWS], an[2][ROWS];
 #pragma unroll
@@ -246,40 +283,41 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
         const bool abort_now = s_abort != 0;
         if (owner) {
             const int pb = t & 1;
-            const float sr = bias_r + rec::tree8([&](int w2) { return part[pb][w2][0][wave][lane]; });
-            const float sz = bias_z + rec::tree8([&](int w2) { return part[pb][w2][1][wave][lane]; });
-            const float sn = bias_n + rec::tree8([&](int w2) { return part[pb][w2][2][wave][lane]; });
-            const float r = rec::sigmoid_f(gxr + sr);
-            const float z = rec::sigmoid_f(gxz + sz);
-            const float n = rec::tanh_f(gxn + r * sn);
+            const float sr = bias_r + rec::tree8([&](int w2) { return part[pb][w2][0][orow][lane]; });
+            const float sz = bias_z + rec::tree8([&](int w2) { return part[pb][w2][1][orow][lane]; });
+            const float sn = bias_n + rec::tree8([&](int w2) { return part[pb][w2][2][orow][lane]; });
+            const float r = rec::sigmoid_f(cur[0] + sr);
+            const float z = rec::sigmoid_f(cur[1] + sz);
+            const float n = rec::tanh_f(cur[2] + r * sn);
             const float h = n + z * (h_prev - n);
             rec::publish_word(exch + (size_t)(t & 1) * B * H + (size_t)prow * H + u,
                               rec::pack_word(h, (unsigned)(t + 1)), xlocal);
-            const size_t bt = (size_t)prow * T + t;
-            y[bt * H + u] = h;
-            if (reserve) {
-                float* cp = reserve + bt * 4 * H;
-                cp[u] = r;
-                cp[H + u] = z;
-                cp[2 * H + u] = n;
-                cp[3 * H + u] = sn;
-            }
+            o_h = h;
+            o_r = r;
+            o_z = z;
+            o_n = n;
+            o_a = sn;
             h_prev = h;
-            if (t + 1 < T) {
-                const float* gp = gx + (bt + 1) * 3 * H;
-                gxr = gp[u];
-                gxz = gp[H + u];
-                gxn = gp[2 * H + u];
-            }
         }
-        if (abort_now) {
+        // @probe:step_end
+        return !abort_now;
+    };
+    bool aborted = false;
+    for (int t = 0; t < T; t += 2) {
+        if (!step(t, gxs[0], gxs[1])) {
             aborted = true;
             break;
         }
-        // @probe:step_end
+        if (t + 1 < T && !step(t + 1, gxs[1], gxs[0])) {
+            aborted = true;
+            break;
+        }
     }
     // @probe:kernel_end
-    if (owner) hn[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : h_prev;
+    if (owner) {
+        if (!aborted) store_outputs(T - 1);
+        hn[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : h_prev;
+    }
 }
 
 // ------------------------------------------------------------ backward ---
