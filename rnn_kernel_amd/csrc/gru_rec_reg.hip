@@ -238,7 +238,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
                     w[e] = rec::load_word(pp[e]);
                 }
             bool ok = true;
-            rec::wait_words<N, true>(pp, pv, w, (unsigned)t, abort_flag, ok);
+            rec::wait_words<N>(pp, pv, w, (unsigned)t, abort_flag, ok);
 #pragma unroll
             for (int q = 0; q < NP; ++q)
 #pragma unroll
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
                     wd[e] = rec::load_word(pp[e]);
                 }
             bool ok = true;
-            rec::wait_words<N, false>(pp, pv, wd, tag, abort_flag, ok);
+            rec::wait_words<N>(pp, pv, wd, tag, abort_flag, ok);
 #pragma unroll
             for (int q = 0; q < NP; ++q)
 #pragma unroll

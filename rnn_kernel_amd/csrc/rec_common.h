@@ -169,127 +169,49 @@ __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int 
     return __builtin_amdgcn_readfirstlane(*s_flag) != 0;
 }
 
-// Re-reads *p until its tag equals `tag` (w holds the first read).  Two
-// loads are kept in flight (each check waits only for the older one), so a
-// word that becomes visible between polls is seen about half a round trip
-// later instead of a full one.  Returns the value; clears `ok` when the spin
-// budget ran out or another workgroup raised the abort flag.
-__device__ __forceinline__ float wait_word(const unsigned long long* p, unsigned long long w, unsigned tag,
-                                           int* abort_flag, bool& ok) {
-    if ((unsigned)(w >> 32) == tag || !ok) return __uint_as_float((unsigned)w);
-    unsigned long long a = load_word(p);
-    int spins = 0;
-    for (;;) {
-        const unsigned long long b = load_word(p);
-        if ((unsigned)(a >> 32) == tag) {
-            w = a;
-            break;
-        }
-        a = load_word(p);
-        if ((unsigned)(b >> 32) == tag) {
-            w = b;
-            break;
-        }
-        spins += 2;
-        if (spins > SPIN_LIMIT) {
-            __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            ok = false;
-            break;
-        }
-        if ((spins & 1023) == 0 &&
-            __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-            ok = false;
-            break;
-        }
-    }
-    return __uint_as_float((unsigned)w);
-}
-
 // Waits for N words of this lane at once: every poll round re-reads all N,
 // so words published together cost one round trip however many there are.
-// PIPELINED keeps two rounds in flight (as wait_word, up to 8 words): a word
-// is seen about half a round trip sooner, but one round is still in flight
-// on return, and the in-order vector-memory counter then makes the first
-// wait on anything issued after the poll cover that round too.  w[] holds the first reads on entry
-// and the matching words on return; a word with valid[v] false counts as
-// ready.  Every p[v] is loaded unconditionally (no exec-mask branches in the
-// loop), so an invalid lane must point at a word that a valid lane of the
-// same instruction loads: the duplicate costs no request, whereas one
-// stand-in address polled by every wave of the grid would be a hot spot.
-template <int N, bool PIPELINED>
+// One round is in flight at a time: measured between two CUs of one XCD on
+// MI355X, a ping-pong round trip is 680 ns with one polling load in flight
+// and 705-920 ns with two to four staggered ones (an L2-hit load takes
+// ~100 ns; the rest is the store becoming visible).  Every word is waited
+// for and tested in each round (no short-circuit), so no load is still
+// pending on return: the in-order vector-memory counter would otherwise
+// make the next wait on anything issued after the poll cover it too.  w[]
+// holds the first reads on entry and the matching words on return; a word
+// with valid[v] false counts as ready.  Every p[v] is loaded
+// unconditionally (no exec-mask branches in the loop), so an invalid lane
+// must point at a word that a valid lane of the same instruction loads: the
+// duplicate costs no request, whereas one stand-in address polled by every
+// wave of the grid would be a hot spot.
+template <int N>
 __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[N], const bool (&valid)[N],
                                            unsigned long long (&w)[N], unsigned tag, int* abort_flag, bool& ok) {
-    // Without pipelining every word is waited for and tested in each round
-    // (no short-circuit): a load still pending at the exit would be waited
-    // for later, at a point where the in-order counter also covers whatever
-    // was issued after it.
-    auto ready = [&](unsigned long long (&x)[N]) {
+    auto ready = [&]() {
         bool r = true;
-        if constexpr (PIPELINED && N <= 8) {
 #pragma unroll
-            for (int v = 0; v < N; ++v) r = r && (!valid[v] || (unsigned)(x[v] >> 32) == tag);
-        } else {
+        for (int v = 0; v < N; ++v) asm volatile("" : "+v"(w[v]));
 #pragma unroll
-            for (int v = 0; v < N; ++v) asm volatile("" : "+v"(x[v]));
-#pragma unroll
-            for (int v = 0; v < N; ++v) r &= (!valid[v] || (unsigned)(x[v] >> 32) == tag);
-        }
+        for (int v = 0; v < N; ++v) r &= (!valid[v] || (unsigned)(w[v] >> 32) == tag);
         return r;
     };
-    if (!ok || ready(w)) return;
+    if (!ok || ready()) return;
     int spins = 0;
-    auto give_up = [&]() {
+    for (;;) {
+#pragma unroll
+        for (int v = 0; v < N; ++v) w[v] = load_word(p[v]);
+        if (ready()) break;
+        ++spins;
         if (spins > SPIN_LIMIT) {
             __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return true;
+            ok = false;
+            break;
         }
-        return (spins & 1023) == 0 &&
-               __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-    };
-    if constexpr (N > 8 || !PIPELINED) {
-        // one round in flight: three register copies of many words would spill,
-        // and a load still in flight after the wait forces the next vmcnt wait
-        // (the counter retires in order) to cover everything issued after it
-        for (;;) {
-#pragma unroll
-            for (int v = 0; v < N; ++v) w[v] = load_word(p[v]);
-            if (ready(w)) break;
-            ++spins;
-            if (give_up()) {
-                ok = false;
-                break;
-            }
-        }
-    } else {
-        unsigned long long a[N], b[N];
-#pragma unroll
-        for (int v = 0; v < N; ++v) a[v] = load_word(p[v]);
-        for (;;) {
-#pragma unroll
-            for (int v = 0; v < N; ++v) b[v] = load_word(p[v]);
-            if (ready(a)) {
-#pragma unroll
-                for (int v = 0; v < N; ++v) w[v] = a[v];
-                break;
-            }
-#pragma unroll
-            for (int v = 0; v < N; ++v) a[v] = load_word(p[v]);
-            if (ready(b)) {
-#pragma unroll
-                for (int v = 0; v < N; ++v) w[v] = b[v];
-                break;
-            }
-            spins += 2;
-            if (give_up()) {
-                ok = false;
-                break;
-            }
+        if ((spins & 1023) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+            ok = false;
+            break;
         }
     }
-}
-
-__device__ __forceinline__ float bcast(float v, int lane) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
 // Row-broadcast FMA: acc += src[16 * (lane / 16) + K] * w on every lane, i.e.
