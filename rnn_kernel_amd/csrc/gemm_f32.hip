@@ -9,10 +9,13 @@
 // blocks.  Operand tiles of 16 (direct) or 32 (split-K) k-steps are staged
 // through LDS in k-major form
 // ([k][row], padded) so that the MFMA operand reads of a half-wave are 32
-// consecutive floats (conflict free); the next tile is prefetched into
-// registers while the current one is consumed (double-buffered LDS, one
-// barrier per tile).  The weight gradients (K = B*T rows) use split-K with a
-// fixed-order reduction, so results are deterministic run to run.
+// consecutive floats (conflict free); the next tile (two tiles for the input
+// projection) is prefetched into registers while the current one is consumed
+// (double-buffered LDS, one barrier per tile).  Each operand layout is a
+// template instance, so no product carries another's address arithmetic
+// (c2: 4-5 % faster than one kernel with runtime layout flags).  The weight
+// gradients (K = B*T rows) use split-K with a fixed-order reduction, so
+// results are deterministic run to run.
 #include "rka_internal.h"
 
 namespace rka {
@@ -25,31 +28,37 @@ constexpr int NT = 256;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-// Address of element (row r, k) of an operand; handles the [h0 ; y[:, :-1]]
-// row remap used as the B operand of dW_hh.
-// SEG: the products of one backward time chunk (SegMap rows); compiled
-// separately so the other products carry no remap arithmetic.
+// Address of element (row r, k) of an operand whose layout is fixed at
+// compile time: KMAJOR 0 = element (r,k) at ptr[r*ld+k], 1 = at ptr[k*ld+r].
+// SHIFT: the [h0 ; y[:, :-1]] row remap of the dW_hh B operand (k = b*T + t
+// reads row k-1 for t > 0 and row b of shift_first for t == 0).  SEG: the
+// products of one backward time chunk (SegMap rows).  Compiled per layout so
+// that no product carries the others' address arithmetic or branches.
 template <bool SEG>
 __device__ __forceinline__ int seg_map(const SegMap& s, int i) {
     if constexpr (!SEG) return i;
     return s.len ? (i / s.len) * s.stride + s.off + i % s.len : i;
 }
 
-template <bool SEG>
+template <int KMAJOR, bool SHIFT, bool SEG>
 __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, int k) {
-    if (op.kmajor == 0) return op.ptr + (size_t)seg_map<SEG>(op.seg, r) * op.ld + k;
-    k = seg_map<SEG>(op.seg, k);
-    if (op.shift_T > 0) {
-        const int t = k % op.shift_T;
-        if (t == 0) return op.shift_first + (size_t)(k / op.shift_T) * op.ld + r;
-        return op.ptr + (size_t)(k - 1) * op.ld + r;
+    if constexpr (KMAJOR == 0) {
+        return op.ptr + (size_t)seg_map<SEG>(op.seg, r) * op.ld + k;
+    } else {
+        k = seg_map<SEG>(op.seg, k);
+        if constexpr (SHIFT) {
+            const int t = k % op.shift_T;
+            if (t == 0) return op.shift_first + (size_t)(k / op.shift_T) * op.ld + r;
+            return op.ptr + (size_t)(k - 1) * op.ld + r;
+        } else {
+            return op.ptr + (size_t)k * op.ld + r;
+        }
     }
-    return op.ptr + (size_t)k * op.ld + r;
 }
 
 // Register staging of one BMxBK operand tile (NV4 float4 per thread).
-// kmajor == 0: thread -> (row tid/KQ + (NT/KQ) i, k 4*(tid%KQ) .. +3), KQ = BK/4
-// kmajor == 1: thread -> (k tid/32 + (NT/32) i, row 4*(tid%32) .. +3)
+// KMAJOR == 0: thread -> (row tid/KQ + (NT/KQ) i, k 4*(tid%KQ) .. +3), KQ = BK/4
+// KMAJOR == 1: thread -> (k tid/32 + (NT/32) i, row 4*(tid%32) .. +3)
 // Direct products (input projection, dx) stage 16 k per tile: three
 // workgroups per CU.  Split-K weight gradients stage 32: half the barriers
 // and twice the MFMA work per load round (two workgroups per CU).
@@ -57,54 +66,54 @@ constexpr int kDirectBK = 16;
 constexpr int kSplitBK = 32;
 static_assert(BM == 128 && BN == 128 && NT == 256, "tile staging layout");
 
-template <bool VEC, bool SEG, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
-__device__ __forceinline__ void load_tile(const GemmOperand& op, int rows, int kend,
-                                          int r0, int k0, int tid, float4 (&v)[NV4]) {
-    if (VEC && r0 + BM <= rows && k0 + BK <= kend) {
-        // interior tile (the common case; the test is uniform): no per-lane
-        // bounds checks, so no exec-mask branches around the loads
+template <int KMAJOR, bool SHIFT, bool SEG, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
+__device__ __forceinline__ void load_tile(const GemmOperand& op, bool vec, int rows, int kend, int r0, int k0,
+                                          int tid, float4 (&v)[NV4]) {
+    if (vec && r0 + BM <= rows && k0 + BK <= kend) {
+        // interior tile of a vector-capable operand (the common case; the
+        // test is uniform): no per-lane bounds checks
 #pragma unroll
         for (int i = 0; i < NV4; ++i) {
-            const int r = op.kmajor == 0 ? r0 + tid / KQ + (NT / KQ) * i : r0 + 4 * (tid % 32);
-            const int k = op.kmajor == 0 ? k0 + 4 * (tid % KQ) : k0 + tid / 32 + (NT / 32) * i;
-            v[i] = *reinterpret_cast<const float4*>(elem_ptr<SEG>(op, r, k));
+            const int r = KMAJOR == 0 ? r0 + tid / KQ + (NT / KQ) * i : r0 + 4 * (tid % 32);
+            const int k = KMAJOR == 0 ? k0 + 4 * (tid % KQ) : k0 + tid / 32 + (NT / 32) * i;
+            v[i] = *reinterpret_cast<const float4*>(elem_ptr<KMAJOR, SHIFT, SEG>(op, r, k));
         }
         return;
     }
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
         int r, k;
-        if (op.kmajor == 0) {
+        if constexpr (KMAJOR == 0) {
             r = r0 + tid / KQ + (NT / KQ) * i;
             k = k0 + 4 * (tid % KQ);
         } else {
             k = k0 + tid / 32 + (NT / 32) * i;
             r = r0 + 4 * (tid % 32);
         }
-        if (VEC) {
-            // Vector path: the contiguous extent is a multiple of 4 and rows
-            // are 16-byte aligned, so a float4 is entirely in or out.
+        if (vec) {
+            // The contiguous extent is a multiple of 4 and rows are 16-byte
+            // aligned, so a float4 is entirely in or out.
             const bool in = (r < rows) && (k < kend);
-            v[i] = in ? *reinterpret_cast<const float4*>(elem_ptr<SEG>(op, r, k))
+            v[i] = in ? *reinterpret_cast<const float4*>(elem_ptr<KMAJOR, SHIFT, SEG>(op, r, k))
                       : make_float4(0.f, 0.f, 0.f, 0.f);
         } else {
             float e[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int rr = op.kmajor == 0 ? r : r + c;
-                const int kk = op.kmajor == 0 ? k + c : k;
-                e[c] = (rr < rows && kk < kend) ? *elem_ptr<SEG>(op, rr, kk) : 0.f;
+                const int rr = KMAJOR == 0 ? r : r + c;
+                const int kk = KMAJOR == 0 ? k + c : k;
+                e[c] = (rr < rows && kk < kend) ? *elem_ptr<KMAJOR, SHIFT, SEG>(op, rr, kk) : 0.f;
             }
             v[i] = make_float4(e[0], e[1], e[2], e[3]);
         }
     }
 }
 
-template <int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
-__device__ __forceinline__ void store_tile(int kmajor, float* lds, int tid, const float4 (&v)[NV4]) {
+template <int KMAJOR, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
+__device__ __forceinline__ void store_tile(float* lds, int tid, const float4 (&v)[NV4]) {
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
-        if (kmajor == 0) {
+        if constexpr (KMAJOR == 0) {
             const int r = tid / KQ + (NT / KQ) * i;
             const int k = 4 * (tid % KQ);
             lds[(k + 0) * LDSP + r] = v[i].x;
@@ -121,6 +130,7 @@ __device__ __forceinline__ void store_tile(int kmajor, float* lds, int tid, cons
 
 struct GemmArgs {
     GemmOperand a, b;
+    int a_vec, b_vec;      // float4 loads allowed (extent, ld and alignment)
     int m, n, k;
     int kchunk;            // k extent per split (multiple of BK)
     const float* bias;     // direct mode
@@ -154,9 +164,125 @@ __device__ __forceinline__ void split_coords(const GemmArgs& p, int& bx, int& by
     by = tile / p.tiles_m;
 }
 
-template <bool AV, bool BV, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
+// MFMAs of one k-tile from LDS (as, bs) into acc; the column sum of A (the
+// bias gradient) rides along for split-K products.
+template <int BK>
+__device__ __forceinline__ void mma_tile(const float* as, const float* bs, int lane, int wm, int wn, int tid,
+                                         bool colsum, float& cs, floatx16 (&acc)[2][2]) {
+    if (colsum && tid < BM) {
+#pragma unroll
+        for (int kk = 0; kk < BK; ++kk) cs += as[kk * LDSP + tid];
+    }
+    // All operand fragments of the tile are read into distinct registers
+    // first: reusing one set per k-step would make every step's LDS reads
+    // wait for the previous step's MFMAs to consume their operands and
+    // leave the matrix core idle for an LDS latency each step.
+    constexpr int KS = BK / 2;
+    float fa0[KS], fa1[KS], fb0[KS], fb1[KS];
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+        const int row = (2 * q + (lane >> 5)) * LDSP + (lane & 31);
+        fa0[q] = as[row + wm * 64];
+        fa1[q] = as[row + wm * 64 + 32];
+        fb0[q] = bs[row + wn * 64];
+        fb1[q] = bs[row + wn * 64 + 32];
+    }
+    // keep the scheduler from sinking the reads back between the MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb0[q], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb1[q], acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[1][1], 0, 0, 0);
+    }
+}
+
+// Interior tiles of vector-capable operands with a whole number of k-tiles
+// (the input projection at the GRU's shapes): operand tiles are
+// prefetched two k-tiles ahead into alternating register sets.  The loads of
+// tile kb+2 are issued before the MFMAs of tile kb and stored to LDS at the
+// end of iteration kb+1, so a load has two MFMA bursts (~1.7 us at BK 16) to
+// arrive.  Every iteration issues the same loads (past the last tile they
+// re-read it), so the wait before an LDS store covers exactly the older set.
+template <int AK, int BKM, bool BSHIFT, bool SEG, int BK>
+__device__ __forceinline__ void mainloop_fast(const GemmArgs& p, int m0, int n0, int kbeg, int nkb, int tid,
+                                              int lane, int wm, int wn, bool colsum, float& cs,
+                                              float (*As)[BK * LDSP], float (*Bs)[BK * LDSP],
+                                              floatx16 (&acc)[2][2]) {
     constexpr int NV4 = BM * BK / (4 * NT);
+    constexpr int KQ = BK / 4;
+    // per-thread base addresses at k = kbeg; a k-tile advances them by a
+    // fixed stride (the row remap of SHIFT is recomputed per tile)
+    auto load = [&](float4 (&ra)[NV4], float4 (&rb)[NV4], int kb) {
+        const int k0 = kbeg + min(kb, nkb - 1) * BK;
+#pragma unroll
+        for (int i = 0; i < NV4; ++i) {
+            const int ra_r = AK == 0 ? m0 + tid / KQ + (NT / KQ) * i : m0 + 4 * (tid % 32);
+            const int ra_k = AK == 0 ? k0 + 4 * (tid % KQ) : k0 + tid / 32 + (NT / 32) * i;
+            ra[i] = *reinterpret_cast<const float4*>(elem_ptr<AK, false, SEG>(p.a, ra_r, ra_k));
+            const int rb_r = BKM == 0 ? n0 + tid / KQ + (NT / KQ) * i : n0 + 4 * (tid % 32);
+            const int rb_k = BKM == 0 ? k0 + 4 * (tid % KQ) : k0 + tid / 32 + (NT / 32) * i;
+            rb[i] = *reinterpret_cast<const float4*>(elem_ptr<BKM, BSHIFT, SEG>(p.b, rb_r, rb_k));
+        }
+    };
+    float4 ra0[NV4], rb0[NV4], ra1[NV4], rb1[NV4];
+    auto step = [&](int kb, int cur, float4 (&fa)[NV4], float4 (&fb)[NV4], float4 (&na)[NV4],
+                    float4 (&nb)[NV4]) {
+        load(fa, fb, kb + 2);
+        mma_tile<BK>(As[cur], Bs[cur], lane, wm, wn, tid, colsum, cs, acc);
+        if (kb + 1 < nkb) {
+            store_tile<AK, BK>(As[cur ^ 1], tid, na);
+            store_tile<BKM, BK>(Bs[cur ^ 1], tid, nb);
+        }
+        __syncthreads();
+    };
+    load(ra0, rb0, 0);
+    load(ra1, rb1, 1);
+    store_tile<AK, BK>(As[0], tid, ra0);
+    store_tile<BKM, BK>(Bs[0], tid, rb0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb += 2) {
+        step(kb, 0, ra0, rb0, ra1, rb1);
+        if (kb + 1 < nkb) step(kb + 1, 1, ra1, rb1, ra0, rb0);
+    }
+}
+
+// Any tile (edges, unaligned or odd-extent operands): one tile of register
+// prefetch, per-element bounds where needed.
+template <int AK, int BKM, bool BSHIFT, bool SEG, int BK>
+__device__ __forceinline__ void mainloop_general(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int nkb,
+                                                 int tid, int lane, int wm, int wn, bool colsum, float& cs,
+                                                 float (*As)[BK * LDSP], float (*Bs)[BK * LDSP],
+                                                 floatx16 (&acc)[2][2]) {
+    constexpr int NV4 = BM * BK / (4 * NT);
+    const bool av = p.a_vec != 0, bv = p.b_vec != 0;
+    float4 ra[NV4], rb[NV4];
+    if (nkb > 0) {
+        load_tile<AK, false, SEG, BK>(p.a, av, p.m, kend, m0, kbeg, tid, ra);
+        load_tile<BKM, BSHIFT, SEG, BK>(p.b, bv, p.n, kend, n0, kbeg, tid, rb);
+        store_tile<AK, BK>(As[0], tid, ra);
+        store_tile<BKM, BK>(Bs[0], tid, rb);
+    }
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int cur = kb & 1;
+        const bool more = kb + 1 < nkb;
+        if (more) {
+            load_tile<AK, false, SEG, BK>(p.a, av, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
+            load_tile<BKM, BSHIFT, SEG, BK>(p.b, bv, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
+        }
+        mma_tile<BK>(As[cur], Bs[cur], lane, wm, wn, tid, colsum, cs, acc);
+        if (more) {
+            store_tile<AK, BK>(As[cur ^ 1], tid, ra);
+            store_tile<BKM, BK>(Bs[cur ^ 1], tid, rb);
+        }
+        __syncthreads();
+    }
+}
+
+template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float As[2][BK * LDSP];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDSP];
 
@@ -182,57 +308,24 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     float cs = 0.f;
 
-    float4 ra[NV4], rb[NV4];
-    if (nkb > 0) {
-        load_tile<AV, SEG, BK>(p.a, p.m, kend, m0, kbeg, tid, ra);
-        load_tile<BV, SEG, BK>(p.b, p.n, kend, n0, kbeg, tid, rb);
-        store_tile<BK>(p.a.kmajor, As[0], tid, ra);
-        store_tile<BK>(p.b.kmajor, Bs[0], tid, rb);
-    }
-    __syncthreads();
-
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int cur = kb & 1;
-        const bool more = kb + 1 < nkb;
-        if (more) {
-            load_tile<AV, SEG, BK>(p.a, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
-            load_tile<BV, SEG, BK>(p.b, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
+    // The two-deep prefetch pays for the input projection (row-major A and
+    // B: 141 vs 145 us at c2) but not for dx (166 vs 137 us) or the split-K
+    // products (257 vs 166 us): its registers cut the resident workgroups
+    // per CU from three to two (one for split-K), so only that layout uses it.
+    constexpr bool kFastLayout = !SPLIT && AK == 0 && BKM == 0;
+    const bool fast = kFastLayout && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 &&
+                      (kend - kbeg) % BK == 0;
+    if constexpr (kFastLayout) {
+        if (fast) {
+            mainloop_fast<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, As, Bs,
+                                                    acc);
+        } else {
+            mainloop_general<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs,
+                                                       As, Bs, acc);
         }
-        const float* as = As[cur];
-        const float* bs = Bs[cur];
-        if (colsum && tid < BM) {
-#pragma unroll
-            for (int kk = 0; kk < BK; ++kk) cs += as[kk * LDSP + tid];
-        }
-        // All operand fragments of the tile are read into distinct registers
-        // first: reusing one set per k-step would make every step's LDS reads
-        // wait for the previous step's MFMAs to consume their operands and
-        // leave the matrix core idle for an LDS latency each step.
-        constexpr int KS = BK / 2;
-        float fa0[KS], fa1[KS], fb0[KS], fb1[KS];
-#pragma unroll
-        for (int q = 0; q < KS; ++q) {
-            const int row = (2 * q + (lane >> 5)) * LDSP + (lane & 31);
-            fa0[q] = as[row + wm * 64];
-            fa1[q] = as[row + wm * 64 + 32];
-            fb0[q] = bs[row + wn * 64];
-            fb1[q] = bs[row + wn * 64 + 32];
-        }
-        // keep the scheduler from sinking the reads back between the MFMAs
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int q = 0; q < KS; ++q) {
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb0[q], acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb1[q], acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[1][1], 0, 0, 0);
-        }
-        if (more) {
-            store_tile<BK>(p.a.kmajor, As[cur ^ 1], tid, ra);
-            store_tile<BK>(p.b.kmajor, Bs[cur ^ 1], tid, rb);
-        }
-        __syncthreads();
-    }
+    } else
+        mainloop_general<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As,
+                                                   Bs, acc);
 
     // Output layout of a 32x32 MFMA block: lane l, register r holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
@@ -298,15 +391,27 @@ bool vec_ok(const GemmOperand& op, int rows, int k) {
 }
 
 template <bool SPLIT, bool SEG>
-int launch_gemm_t(const GemmArgs& args, dim3 grid, bool av, bool bv, hipStream_t stream) {
-    if (av && bv) {
-        hipLaunchKernelGGL((gemm_f32_kernel<true, true, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
-    } else if (av) {
-        hipLaunchKernelGGL((gemm_f32_kernel<true, false, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
-    } else if (bv) {
-        hipLaunchKernelGGL((gemm_f32_kernel<false, true, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
+int launch_gemm_t(const GemmArgs& args, dim3 grid, hipStream_t stream) {
+    const int ak = args.a.kmajor, bk = args.b.kmajor;
+    const bool shift = args.b.shift_T > 0;
+    if (shift && !bk) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: the row remap needs a k-major operand");
+    if (SPLIT) {
+        // the weight gradients: both operands k-major
+        if (!ak || !bk) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: split-K products take k-major operands");
+        if (shift)
+            hipLaunchKernelGGL((gemm_f32_kernel<1, 1, true, true, SEG>), grid, dim3(NT), 0, stream, args);
+        else
+            hipLaunchKernelGGL((gemm_f32_kernel<1, 1, false, true, SEG>), grid, dim3(NT), 0, stream, args);
     } else {
-        hipLaunchKernelGGL((gemm_f32_kernel<false, false, SPLIT, SEG>), grid, dim3(NT), 0, stream, args);
+        if (shift) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: the row remap is for split-K products");
+        if (!ak && !bk)
+            hipLaunchKernelGGL((gemm_f32_kernel<0, 0, false, false, SEG>), grid, dim3(NT), 0, stream, args);
+        else if (!ak)
+            hipLaunchKernelGGL((gemm_f32_kernel<0, 1, false, false, SEG>), grid, dim3(NT), 0, stream, args);
+        else if (!bk)
+            hipLaunchKernelGGL((gemm_f32_kernel<1, 0, false, false, SEG>), grid, dim3(NT), 0, stream, args);
+        else
+            hipLaunchKernelGGL((gemm_f32_kernel<1, 1, false, false, SEG>), grid, dim3(NT), 0, stream, args);
     }
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
@@ -318,14 +423,15 @@ int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream)
     args.tiles_m = tm;
     args.tiles = tm * tn;
     args.ksplit = ksplit;
+    args.a_vec = av ? 1 : 0;
+    args.b_vec = bv ? 1 : 0;
     if (!SPLIT) {
         args.z_off = 0;
         args.ksplit_total = 1;
     }
     const dim3 grid = SPLIT ? dim3(tm * tn * ksplit) : dim3(tm, tn);
     const bool seg = args.a.seg.len || args.b.seg.len || args.c_seg.len;
-    return seg ? launch_gemm_t<SPLIT, true>(args, grid, av, bv, stream)
-               : launch_gemm_t<SPLIT, false>(args, grid, av, bv, stream);
+    return seg ? launch_gemm_t<SPLIT, true>(args, grid, stream) : launch_gemm_t<SPLIT, false>(args, grid, stream);
 }
 
 }  // namespace
