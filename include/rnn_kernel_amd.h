@@ -190,6 +190,50 @@ int rka_profile_enable(int on);
 int rka_profile_read(double ms_out[RKA_NUM_STAGES], int count_out[RKA_NUM_STAGES]);
 const char* rka_profile_stage_name(int stage);
 
+/*
+ * Training-step operations on either side of the GRU in the reference's
+ * benchmark harness (rnn_benchmark.py:510,525,636,722): the Linear(H, 1)
+ * head, the mean-squared-error loss and the AdamW update, which the
+ * reference runs as PyTorch ops (nn.Linear, F.mse_loss, torch.optim.AdamW).
+ * Every reduction runs in a fixed order (bitwise reproducible).
+ */
+
+/* Workspace bytes of rka_mse_forward for n elements. */
+size_t rka_mse_workspace_bytes(size_t n);
+
+/* loss[0] = sum_i (pred_i - target_i)^2 / n  (F.mse_loss, reduction 'mean',
+ * rnn_benchmark.py:636). */
+int rka_mse_forward(const float* pred, const float* target, float* loss, void* workspace, size_t workspace_bytes,
+                    size_t n, void* stream);
+
+/* grad_pred_i = grad_loss[0] * 2 (pred_i - target_i) / n  (its backward). */
+int rka_mse_backward(const float* pred, const float* target, const float* grad_loss, float* grad_pred, size_t n,
+                     void* stream);
+
+/* pred[r] = sum_h out[r, h] w[h] + b[0] for rows r < rows of out [rows, hidden]
+ * (self.head = nn.Linear(hidden_size, 1); head(out).squeeze(-1),
+ * rnn_benchmark.py:510,525). */
+int rka_head_forward(const float* out, const float* w, const float* b, float* pred, int rows, int hidden,
+                     void* stream);
+
+/* Workspace bytes of rka_head_backward. */
+size_t rka_head_backward_workspace_bytes(int rows, int hidden);
+
+/* dout[r, h] = dpred[r] w[h] (skipped when dout is NULL),
+ * dw[h] = sum_r dpred[r] out[r, h], db[0] = sum_r dpred[r]. */
+int rka_head_backward(const float* out, const float* w, const float* dpred, float* dout, float* dw, float* db,
+                      void* workspace, size_t workspace_bytes, int rows, int hidden, void* stream);
+
+/* One AdamW step (torch.optim.AdamW: decoupled weight decay, bias-corrected
+ * moments; rnn_benchmark.py:722) over `count` tensors: params[i], grads[i],
+ * exp_avgs[i], exp_avg_sqs[i] are device pointers of numels[i] floats; the
+ * pointer arrays themselves are host memory.  `step` counts from 1.  The
+ * hyper-parameters are doubles: scalars such as 1 - beta2 are formed in
+ * double and rounded to fp32 once, as torch forms them from Python floats. */
+int rka_adamw_step(float* const* params, const float* const* grads, float* const* exp_avgs,
+                   float* const* exp_avg_sqs, const size_t* numels, int count, double lr, double beta1,
+                   double beta2, double eps, double weight_decay, int step, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

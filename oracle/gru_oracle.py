@@ -168,3 +168,75 @@ def stack_forward_backward(x, hx, params: Sequence[dict], dy, dhn=None, dtype=np
         dhx[l] = b.dh0
         g_out = b.dx
     return StackResult(fwds[-1].y, np.stack(hns, 0), g_out, dhx, grads)
+
+
+# ------------------------------------------------ harness-side operations ---
+# float64 restatements of the benchmark harness's head, loss and optimiser
+# (train_ops_oracle.c; reference rnn_benchmark.py:510,525,636,722).
+def _load_train():
+    lib = _load()
+    if not getattr(lib, "_train_ready", False):
+        D, P, I, SZ = ctypes.c_double, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        lib.oracle_head_forward_f64.restype = None
+        lib.oracle_head_forward_f64.argtypes = [I, I, P, P, D, P]
+        lib.oracle_head_backward_f64.restype = None
+        lib.oracle_head_backward_f64.argtypes = [I, I, P, P, P, P, P, P]
+        lib.oracle_mse_forward_f64.restype = D
+        lib.oracle_mse_forward_f64.argtypes = [SZ, P, P]
+        lib.oracle_mse_backward_f64.restype = None
+        lib.oracle_mse_backward_f64.argtypes = [SZ, P, P, D, P]
+        lib.oracle_adamw_step_f64.restype = None
+        lib.oracle_adamw_step_f64.argtypes = [SZ, P, P, P, P, D, D, D, D, D, I]
+        lib._train_ready = True
+    return lib
+
+
+def head_forward(out, w, b) -> np.ndarray:
+    """pred[r] = out[r] . w + b for out [..., H] (leading dims flattened)."""
+    lib = _load_train()
+    out = _c(out, np.float64)
+    lead = out.shape[:-1]
+    H = out.shape[-1]
+    rows = int(np.prod(lead)) if lead else 1
+    w = _c(np.reshape(w, (H,)), np.float64)
+    pred = np.empty(rows, dtype=np.float64)
+    lib.oracle_head_forward_f64(rows, H, _p(out), _p(w), float(np.reshape(b, (-1,))[0]), _p(pred))
+    return pred.reshape(lead)
+
+
+def head_backward(out, w, dpred, need_dout: bool = True):
+    """Returns (dout [..., H] or None, dw [H], db scalar)."""
+    lib = _load_train()
+    out = _c(out, np.float64)
+    H = out.shape[-1]
+    rows = out.size // H
+    w = _c(np.reshape(w, (H,)), np.float64)
+    dpred = _c(np.reshape(dpred, (rows,)), np.float64)
+    dout = np.empty_like(out) if need_dout else None
+    dw = np.empty(H, dtype=np.float64)
+    db = np.zeros(1, dtype=np.float64)
+    lib.oracle_head_backward_f64(rows, H, _p(out), _p(w), _p(dpred), _p(dout), _p(dw), _p(db))
+    return dout, dw, float(db[0])
+
+
+def mse_forward(pred, target) -> float:
+    lib = _load_train()
+    pred, target = _c(pred, np.float64), _c(target, np.float64)
+    assert pred.shape == target.shape
+    return float(lib.oracle_mse_forward_f64(pred.size, _p(pred), _p(target)))
+
+
+def mse_backward(pred, target, grad_loss: float = 1.0) -> np.ndarray:
+    lib = _load_train()
+    pred, target = _c(pred, np.float64), _c(target, np.float64)
+    grad = np.empty_like(pred)
+    lib.oracle_mse_backward_f64(pred.size, _p(pred), _p(target), float(grad_loss), _p(grad))
+    return grad
+
+
+def adamw_step(p, g, m, v, lr, beta1, beta2, eps, weight_decay, step):
+    """One AdamW step; returns new (p, m, v) as float64 arrays."""
+    lib = _load_train()
+    p, g, m, v = (np.array(a, dtype=np.float64, copy=True) for a in (p, g, m, v))
+    lib.oracle_adamw_step_f64(p.size, _p(p), _p(g), _p(m), _p(v), lr, beta1, beta2, eps, weight_decay, int(step))
+    return p, m, v

@@ -9,8 +9,14 @@ from .gru import (
     is_available,
     is_supported_gru,
 )
+from .train import AdamW, HeadFunction, LinearHead, MSELossFunction, mse_loss
 
 __all__ = [
+    "AdamW",
+    "HeadFunction",
+    "LinearHead",
+    "MSELossFunction",
+    "mse_loss",
     "GRU",
     "GRUFunction",
     "MAX_HIDDEN_SIZE",

@@ -40,6 +40,13 @@ SIGNATURES = {
     "rka_profile_enable": (_I, [_I]),
     "rka_profile_read": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "rka_profile_stage_name": (ctypes.c_char_p, [_I]),
+    "rka_mse_workspace_bytes": (_SZ, [_SZ]),
+    "rka_mse_forward": (_I, [_P, _P, _P, _P, _SZ, _SZ, _P]),
+    "rka_mse_backward": (_I, [_P, _P, _P, _P, _SZ, _P]),
+    "rka_head_forward": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "rka_head_backward_workspace_bytes": (_SZ, [_I, _I]),
+    "rka_head_backward": (_I, [_P] * 7 + [_SZ, _I, _I, _P]),
+    "rka_adamw_step": (_I, [ctypes.POINTER(_P)] * 4 + [ctypes.POINTER(_SZ), _I] + [ctypes.c_double] * 5 + [_I, _P]),
 }
 NUM_STAGES = 6
 

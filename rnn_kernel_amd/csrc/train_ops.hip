@@ -1,0 +1,301 @@
+// Training-step operations on either side of the GRU in the reference's
+// benchmark harness: the Linear(H, 1) head, the mean-squared-error loss and
+// the AdamW update (rnn_benchmark.py:510,526,618-639).  All of them are
+// HBM-bound elementwise passes or reductions; every reduction runs in a
+// fixed order (per-block partial sums, then one ordered pass over the
+// partials), so results are bitwise reproducible run to run.
+#include "rka_internal.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace rka {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxReduceBlocks = 1024;   // partial sums of a loss reduction
+constexpr int kHeadBlocks = 512;         // row ranges of the head's dw reduction
+
+// Sum over the block's threads in a fixed tree order; the result is valid in
+// thread 0.  `scratch` holds kThreads floats.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    scratch[threadIdx.x] = v;
+    __syncthreads();
+#pragma unroll
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) scratch[threadIdx.x] += scratch[threadIdx.x + s];
+        __syncthreads();
+    }
+    return scratch[0];
+}
+
+// ------------------------------------------------------------------ MSE ---
+// Block b sums (pred - target)^2 over its contiguous range of `chunk`
+// elements (thread t: elements t, t + 256, ... of the range).
+__global__ __launch_bounds__(kThreads) void mse_partial_kernel(const float* __restrict__ pred,
+                                                               const float* __restrict__ target, size_t n,
+                                                               size_t chunk, float* __restrict__ partial) {
+    __shared__ float scratch[kThreads];
+    const size_t beg = (size_t)blockIdx.x * chunk;
+    const size_t end = beg + chunk < n ? beg + chunk : n;
+    float acc = 0.f;
+    for (size_t i = beg + threadIdx.x; i < end; i += kThreads) {
+        const float d = pred[i] - target[i];
+        acc = fmaf(d, d, acc);
+    }
+    const float s = block_sum(acc, scratch);
+    if (threadIdx.x == 0) partial[blockIdx.x] = s;
+}
+
+// loss[0] = (sum of the nb partials, thread t summing t, t + 256, ... in
+// order, then the fixed tree) / n
+__global__ __launch_bounds__(kThreads) void mse_finish_kernel(const float* __restrict__ partial, int nb, size_t n,
+                                                              float* __restrict__ loss) {
+    __shared__ float scratch[kThreads];
+    float acc = 0.f;
+    for (int i = threadIdx.x; i < nb; i += kThreads) acc += partial[i];
+    const float s = block_sum(acc, scratch);
+    if (threadIdx.x == 0) loss[0] = s / (float)n;
+}
+
+// grad_pred = grad_loss * 2 (pred - target) / n  (torch's mse_loss backward
+// for reduction='mean': norm = 2 / n, grad = norm * (pred - target) * grad)
+__global__ __launch_bounds__(kThreads) void mse_backward_kernel(const float* __restrict__ pred,
+                                                                const float* __restrict__ target,
+                                                                const float* __restrict__ grad_loss, size_t n,
+                                                                float* __restrict__ grad_pred) {
+    const float norm = 2.0f / (float)n;
+    const float g = grad_loss[0];
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (size_t)gridDim.x * kThreads)
+        grad_pred[i] = norm * (pred[i] - target[i]) * g;
+}
+
+int mse_blocks(size_t n, size_t* chunk) {
+    const size_t nb = std::min<size_t>(kMaxReduceBlocks, (n + 4095) / 4096);
+    const size_t b = nb < 1 ? 1 : nb;
+    *chunk = (n + b - 1) / b;
+    return (int)b;
+}
+
+// ----------------------------------------------------------------- head ---
+// pred[r] = sum_h out[r, h] w[h] + b[0]; one wavefront per row, lane l
+// summing h = l, l + 64, ... in order, then a fixed butterfly across lanes.
+__global__ __launch_bounds__(kThreads) void head_forward_kernel(const float* __restrict__ out,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ b, int rows, int hidden,
+                                                                float* __restrict__ pred) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* o = out + (size_t)row * hidden;
+    float acc = 0.f;
+    for (int h = lane; h < hidden; h += 64) acc = fmaf(o[h], w[h], acc);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) pred[row] = acc + b[0];
+}
+
+// dout[r, h] = dpred[r] w[h] (if dout), and per row range of block k:
+// partial[k][h] = sum_r dpred[r] out[r, h], partial[k][hidden] = sum_r dpred[r]
+// (rows in order, thread t owning h = t, t + 256, ...).
+__global__ __launch_bounds__(kThreads) void head_backward_partial_kernel(
+    const float* __restrict__ out, const float* __restrict__ w, const float* __restrict__ dpred, int rows,
+    int hidden, int rows_per_block, float* __restrict__ dout, float* __restrict__ partial) {
+    const int r0 = blockIdx.x * rows_per_block;
+    const int r1 = min(rows, r0 + rows_per_block);
+    float* part = partial + (size_t)blockIdx.x * (hidden + 1);
+    for (int h = threadIdx.x; h <= hidden; h += kThreads) {
+        const bool bias = h == hidden;
+        const float wh = bias ? 0.f : w[h];
+        float acc = 0.f;
+#pragma unroll 8
+        for (int r = r0; r < r1; ++r) {
+            const float g = dpred[r];
+            if (bias) {
+                acc += g;
+            } else {
+                const size_t idx = (size_t)r * hidden + h;
+                acc = fmaf(g, out[idx], acc);
+                if (dout) dout[idx] = g * wh;
+            }
+        }
+        part[h] = acc;
+    }
+}
+
+// dw[h] = sum_k partial[k][h] (k in order); db[0] = sum_k partial[k][hidden]
+__global__ __launch_bounds__(kThreads) void head_backward_finish_kernel(const float* __restrict__ partial, int nb,
+                                                                        int hidden, float* __restrict__ dw,
+                                                                        float* __restrict__ db) {
+    const int h = blockIdx.x * kThreads + threadIdx.x;
+    if (h > hidden) return;
+    float acc = 0.f;
+    for (int k = 0; k < nb; ++k) acc += partial[(size_t)k * (hidden + 1) + h];
+    if (h < hidden)
+        dw[h] = acc;
+    else
+        db[0] = acc;
+}
+
+int head_blocks(int rows, int* rows_per_block) {
+    const int nb = std::max(1, std::min(kHeadBlocks, rows));
+    *rows_per_block = (rows + nb - 1) / nb;
+    return (rows + *rows_per_block - 1) / *rows_per_block;
+}
+
+// ---------------------------------------------------------------- AdamW ---
+constexpr int kAdamMaxTensors = 16;
+
+struct AdamTensor {
+    float* p;
+    const float* g;
+    float* m;
+    float* v;
+    size_t n;
+};
+
+struct AdamArgs {
+    AdamTensor t[kAdamMaxTensors];
+    int count;
+    float beta2, eps;
+    // scalars formed in double on the host and rounded once, as torch forms
+    // them from Python floats (1 - beta2 is not 1 - (float)beta2)
+    float decay;           // 1 - lr * weight_decay
+    float w1, w2;          // 1 - beta1, 1 - beta2
+    float step_size;       // lr / (1 - beta1^step)
+    float bc2_sqrt;        // sqrt(1 - beta2^step)
+};
+
+// torch.optim.AdamW's update (decoupled weight decay), in its order:
+//   p *= 1 - lr wd;  m = lerp(m, g, 1 - beta1);  v = beta2 v + (1 - beta2) g^2
+//   p -= step_size * m / (sqrt(v) / sqrt(1 - beta2^step) + eps)
+// grid.y = tensor, grid.x strides over its elements.
+__global__ __launch_bounds__(kThreads) void adamw_kernel(AdamArgs a) {
+    const AdamTensor t = a.t[blockIdx.y];
+    const float decay = a.decay, w1 = a.w1, w2 = a.w2;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < t.n; i += (size_t)gridDim.x * kThreads) {
+        const float g = t.g[i];
+        float p = t.p[i] * decay;
+        // lerp(m, g, w) with w < 0.5: m + w (g - m)
+        const float m = t.m[i] + w1 * (g - t.m[i]);
+        const float v = t.v[i] * a.beta2 + w2 * g * g;
+        const float denom = sqrtf(v) / a.bc2_sqrt + a.eps;
+        p = p - a.step_size * (m / denom);
+        t.p[i] = p;
+        t.m[i] = m;
+        t.v[i] = v;
+    }
+}
+
+}  // namespace
+}  // namespace rka
+
+using namespace rka;
+
+extern "C" {
+
+size_t rka_mse_workspace_bytes(size_t n) {
+    size_t chunk = 0;
+    return (size_t)mse_blocks(n, &chunk) * sizeof(float);
+}
+
+int rka_mse_forward(const float* pred, const float* target, float* loss, void* workspace, size_t workspace_bytes,
+                    size_t n, void* stream) {
+    if (n == 0 || !pred || !target || !loss) return fail(RKA_ERR_INVALID_ARGUMENT, "mse_forward: bad arguments");
+    size_t chunk = 0;
+    const int nb = mse_blocks(n, &chunk);
+    if (!workspace || workspace_bytes < (size_t)nb * sizeof(float))
+        return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "mse_forward: workspace too small");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    float* partial = reinterpret_cast<float*>(workspace);
+    hipLaunchKernelGGL(mse_partial_kernel, dim3(nb), dim3(kThreads), 0, s, pred, target, n, chunk, partial);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    hipLaunchKernelGGL(mse_finish_kernel, dim3(1), dim3(kThreads), 0, s, partial, nb, n, loss);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+int rka_mse_backward(const float* pred, const float* target, const float* grad_loss, float* grad_pred, size_t n,
+                     void* stream) {
+    if (n == 0 || !pred || !target || !grad_loss || !grad_pred)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "mse_backward: bad arguments");
+    const size_t blocks = std::min<size_t>((n + kThreads - 1) / kThreads, 4096);
+    hipLaunchKernelGGL(mse_backward_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), pred, target, grad_loss, n, grad_pred);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+int rka_head_forward(const float* out, const float* w, const float* b, float* pred, int rows, int hidden,
+                     void* stream) {
+    if (rows < 1 || hidden < 1 || !out || !w || !b || !pred)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "head_forward: bad arguments");
+    const int per_block = kThreads / 64;
+    hipLaunchKernelGGL(head_forward_kernel, dim3((rows + per_block - 1) / per_block), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), out, w, b, rows, hidden, pred);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+size_t rka_head_backward_workspace_bytes(int rows, int hidden) {
+    if (rows < 1 || hidden < 1) return 0;
+    int rpb = 0;
+    const int nb = head_blocks(rows, &rpb);
+    return (size_t)nb * (hidden + 1) * sizeof(float);
+}
+
+int rka_head_backward(const float* out, const float* w, const float* dpred, float* dout, float* dw, float* db,
+                      void* workspace, size_t workspace_bytes, int rows, int hidden, void* stream) {
+    if (rows < 1 || hidden < 1 || !out || !w || !dpred || !dw || !db)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "head_backward: bad arguments");
+    int rpb = 0;
+    const int nb = head_blocks(rows, &rpb);
+    if (!workspace || workspace_bytes < (size_t)nb * (hidden + 1) * sizeof(float))
+        return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "head_backward: workspace too small");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    float* partial = reinterpret_cast<float*>(workspace);
+    hipLaunchKernelGGL(head_backward_partial_kernel, dim3(nb), dim3(kThreads), 0, s, out, w, dpred, rows, hidden, rpb,
+                       dout, partial);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    hipLaunchKernelGGL(head_backward_finish_kernel, dim3((hidden + 1 + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                       s, partial, nb, hidden, dw, db);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+int rka_adamw_step(float* const* params, const float* const* grads, float* const* exp_avgs,
+                   float* const* exp_avg_sqs, const size_t* numels, int count, double lr, double beta1,
+                   double beta2, double eps, double weight_decay, int step, void* stream) {
+    if (count < 0 || (count > 0 && (!params || !grads || !exp_avgs || !exp_avg_sqs || !numels)) || step < 1)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "adamw_step: bad arguments");
+    // bias corrections in double, as torch computes them from Python floats
+    const double bc1 = 1.0 - std::pow(beta1, (double)step);
+    const double bc2 = 1.0 - std::pow(beta2, (double)step);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    for (int first = 0; first < count; first += kAdamMaxTensors) {
+        AdamArgs a{};
+        a.count = std::min(kAdamMaxTensors, count - first);
+        size_t max_n = 0;
+        for (int i = 0; i < a.count; ++i) {
+            const int j = first + i;
+            if (!params[j] || !grads[j] || !exp_avgs[j] || !exp_avg_sqs[j])
+                return fail(RKA_ERR_INVALID_ARGUMENT, "adamw_step: null tensor pointer");
+            a.t[i] = AdamTensor{params[j], grads[j], exp_avgs[j], exp_avg_sqs[j], numels[j]};
+            max_n = std::max(max_n, numels[j]);
+        }
+        if (max_n == 0) continue;
+        a.beta2 = (float)beta2;
+        a.eps = (float)eps;
+        a.decay = (float)(1.0 - lr * weight_decay);
+        a.w1 = (float)(1.0 - beta1);
+        a.w2 = (float)(1.0 - beta2);
+        a.step_size = (float)(lr / bc1);
+        a.bc2_sqrt = (float)std::sqrt(bc2);
+        const unsigned gx = (unsigned)std::min<size_t>((max_n + kThreads - 1) / kThreads, 1024);
+        hipLaunchKernelGGL(adamw_kernel, dim3(gx, a.count), dim3(kThreads), 0, s, a);
+        RKA_RETURN_IF_HIP(hipGetLastError());
+    }
+    return 0;
+}
+
+}  // extern "C"
