@@ -5,7 +5,9 @@ Workload = BASELINE config 2: 1-layer GRU, input 256, hidden 256, batch 64,
 seq_len 512, fp32; x ~ N(0,1), PyTorch-uniform init, h0 ~ 0.1 N(0,1), MSE loss
 against an N(0,1) target; a step is forward + loss + backward producing the
 gradients of all four weight/bias tensors, x and h0 (no optimizer, as the
-reference's published fwd+bwd numbers).  Inputs are generated on the CPU with
+reference's published fwd+bwd numbers).  The MSE loss is the library's
+(rnn_kernel_amd.mse_loss, the same mean squared error as F.mse_loss); the
+torch.nn.GRU baselines use F.mse_loss.  Inputs are generated on the CPU with
 seed 42, copied to the GPU, and resident in HBM before timing starts.
 
 Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
@@ -89,9 +91,10 @@ def make_inputs():
     return gru, x, h0, target
 
 
-def time_steps(model, x, h0, target, steps, warmup, sync, profile_cb=None):
-    import torch
+def time_steps(model, x, h0, target, steps, warmup, sync, profile_cb=None, loss_fn=None):
     import torch.nn.functional as F
+
+    loss_fn = loss_fn or F.mse_loss
 
     def step():
         for p in model.parameters():
@@ -99,7 +102,7 @@ def time_steps(model, x, h0, target, steps, warmup, sync, profile_cb=None):
         x.grad = None
         h0.grad = None
         out, hn = model(x, h0)
-        loss = F.mse_loss(out, target)
+        loss = loss_fn(out, target)
         loss.backward()
 
     for _ in range(warmup):
@@ -187,7 +190,7 @@ def main():
 
     import torch
 
-    from rnn_kernel_amd import _lib, from_torch_gru
+    from rnn_kernel_amd import _lib, from_torch_gru, mse_loss
 
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
@@ -202,11 +205,12 @@ def main():
     ours = from_torch_gru(gru.to(dev))
 
     _lib.profile_read()  # clear
-    t_step = time_steps(ours, x, h0, target, args.steps, args.warmup, sync, profile_cb=_lib.profile_enable)
+    t_step = time_steps(ours, x, h0, target, args.steps, args.warmup, sync, profile_cb=_lib.profile_enable,
+                        loss_fn=mse_loss)
     stages = _lib.profile_read()
     _lib.profile_enable(False)
     # second timed pass without event records for the headline number
-    t_step_noprof = time_steps(ours, x, h0, target, args.steps, 0, sync)
+    t_step_noprof = time_steps(ours, x, h0, target, args.steps, 0, sync, loss_fn=mse_loss)
     t_step = min(t_step, t_step_noprof)
 
     # per-step stage totals; a stage may run as several launches per step
