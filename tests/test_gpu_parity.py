@@ -114,6 +114,9 @@ LAYER_SHAPES = [
     (5, 3, 2, 1),        # H = 1
     (1, 1, 1, 64),       # single step, single row
     (9, 6, 5, 96),       # batch not a multiple of the row group
+    (3, 6, 5, 200),      # four slices, the last one partial (float4 weight loads)
+    (2, 5, 3, 221),      # four slices, H not a multiple of 4 (scalar weight loads)
+    (4, 4, 2, 193),      # four slices, one unit in the last
 ]
 
 
@@ -194,6 +197,7 @@ def backward_chunks(hip_lib):
     (4, 5, 3, 256, 3),     # register kernel at H = 256
     (2, 3, 2, 40, 8),      # more chunks asked than steps: clamped to T
     (8, 9, 4, 256, 3),     # H = 256 with groups on one XCD (plain publishing stores) across ranges
+    (3, 8, 4, 200, 3),     # four slices, the last one partial, across ranges
 ])
 def test_chunked_backward_matches_oracle(gpu, oracle, rec_kind, backward_chunks, B, T, I, H, chunks):
     """The backward in time chunks (recurrence per range, gradient GEMMs of a
@@ -494,7 +498,7 @@ def test_config2_north_star_matches_torch_gru_and_oracle_rows(gpu, oracle):
     assert _rel(res["ours"]["dh0"][0, rows], b.dh0) <= GRAD_REL
 
 
-@pytest.mark.parametrize("H", [64, 96, 128, 129, 130, 160, 192])
+@pytest.mark.parametrize("H", [64, 96, 128, 129, 130, 160, 192, 224])
 def test_config3_hidden_sweep_matches_torch_gru(gpu, H):
     print(f"config3 H={H}", flush=True)
     res, _ = _torch_reference(gpu, 1, H, H, 64, 512, seed=42 + H, h0_scale=0.1)
