@@ -461,6 +461,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         rec::dpp_src_guard(hl);
         dot_range3<0, 8>(ar, az, an, hl, wr, wz, wn);
     };
+    unsigned long long first_read = 0;
     // step 0's own slot from h0 (lane K of each row: k = kof(0, K))
     {
         const int k = kof(0, lane & 7);
@@ -475,7 +476,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
             const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H + (size_t)row * H;
             const unsigned long long* pp[1] = {src + pidx};
             const bool pv[1] = {pvalid};
-            unsigned long long w[1] = {rec::load_word(pp[0])};
+            unsigned long long w[1] = {first_read};
             bool ok = true;
             rec::wait_words<1>(pp, pv, w, (unsigned)t, abort_flag, ok);
             hx = pvalid ? __uint_as_float((unsigned)w[0]) : 0.f;
@@ -520,8 +521,13 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         }
         if (wave == 0) hloc[t & 1][lane] = owner ? h_prev : 0.f;  // zero past H
         __syncthreads();
-        // the own slot of step t+1 while the other slices' words travel
-        if (t + 1 < T) local_fmas(hloc[t & 1][8 * wave + (lane & 7)]);
+        // @probe:released
+        // the own slot of step t+1 while the other slices' words travel,
+        // with the first poll read of step t+1 already in flight
+        if (t + 1 < T) {
+            first_read = rec::load_word(exch + (size_t)(t & 1) * B * H + (size_t)row * H + pidx);
+            local_fmas(hloc[t & 1][8 * wave + (lane & 7)]);
+        }
         // @probe:step_end
         return !abort_now;
     };
@@ -848,6 +854,13 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         }
     };
     float acc[8];
+    // the first poll reads of step i, issued ahead of its own-slot FMAs
+    unsigned long long first_read[2] = {0, 0};
+    auto first_poll = [&](int i) {
+        const unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3 + (size_t)row * H3;
+        first_read[0] = rec::load_word(slotp + pidx0);
+        first_read[1] = rec::load_word(slotp + pidx1);
+    };
     auto local_fmas = [&]() {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
@@ -868,7 +881,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         {
             const unsigned long long* pp[2] = {slotp + pidx0, slotp + pidx1};
             const bool pv[2] = {pv0, pv1};
-            unsigned long long wd[2] = {rec::load_word(pp[0]), rec::load_word(pp[1])};
+            unsigned long long wd[2] = {first_read[0], first_read[1]};
             bool ok = true;
             rec::wait_words<2>(pp, pv, wd, (unsigned)(i + 1), abort_flag, ok);
             gr0 = pv0 ? __uint_as_float((unsigned)wd[0]) : 0.f;
@@ -903,13 +916,19 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         if (owner) dh = ddirect + rec::tree8([&](int w2) { return part[i & 1][w2][lane]; });
         const bool more = i + 1 < i1;
         if (more) pointwise(i + 1, nxt);
+        // @probe:published
         __syncthreads();
-        if (more) local_fmas();
+        // @probe:released
+        if (more) {
+            first_poll(i + 1);
+            local_fmas();
+        }
         // @probe:step_end
         return !abort_now;
     };
     if (i0 < i1) pointwise(i0, ins[0]);
     __syncthreads();
+    first_poll(i0);
     local_fmas();
     bool aborted = false;
     for (int i = i0; i < i1; i += 2) {
