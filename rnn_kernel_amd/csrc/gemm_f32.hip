@@ -1,21 +1,25 @@
-// fp32 GEMMs of the GRU path on gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
+// fp32 GEMMs of the GRU path on gfx950 matrix cores (v_mfma_f32_16x16x4_f32).
 //
 // One kernel template serves the four products of a layer:
 //   input projection  Gx  = X W_ih^T + b_ih        (A row-major, B row-major)
 //   input gradient    dX  = G_i W_ih               (A row-major, B k-major)
 //   weight gradients  dW  = G^T [X | Hprev]        (A k-major,  B k-major)
 // C[m,n] = sum_k A(m,k) B(n,k).  A workgroup of 4 wavefronts computes a
-// 128x128 tile; each wavefront owns a 64x64 quadrant as 2x2 MFMA 32x32
-// blocks.  Operand tiles of 16 (direct) or 32 (split-K) k-steps are staged
-// through LDS in k-major form
-// ([k][row], padded) so that the MFMA operand reads of a half-wave are 32
-// consecutive floats (conflict free); the next tile (two tiles for the input
-// projection) is prefetched into registers while the current one is consumed
-// (double-buffered LDS, one barrier per tile).  Each operand layout is a
-// template instance, so no product carries another's address arithmetic
-// (c2: 4-5 % faster than one kernel with runtime layout flags).  The weight
-// gradients (K = B*T rows) use split-K with a fixed-order reduction, so
-// results are deterministic run to run.
+// 128x128 tile; each wavefront owns a 64x64 quadrant as 4x4 MFMA 16x16
+// blocks.  Operand tiles of 16 (direct) or 32 (split-K) k are staged through
+// double-buffered LDS (the next tile is loaded into registers while the
+// current one is consumed; one barrier per tile).  The LDS forms are chosen
+// so that every MFMA operand read is one conflict-free ds_read_b128 feeding
+// four MFMAs: A keeps the form of its global layout (row-major tiles give a
+// lane four k of one row, k-major tiles four rows at one k) and B is kept
+// k-major, which also makes a lane's four B blocks four adjacent output
+// columns, stored as one float4.  Measured at c2 against the previous
+// v_mfma_f32_32x32x2_f32 kernel (b32 operand reads, scalar stores): input
+// projection 128 vs 141 us, dx 126 vs 133 us, dW 157/148 vs 161/154 us.
+// Each operand layout is a template instance, so no product carries
+// another's address arithmetic.  The weight gradients (K = B*T rows) use
+// split-K with a fixed-order reduction, so results are deterministic run to
+// run.
 #include "rka_internal.h"
 
 namespace rka {
@@ -26,7 +30,7 @@ constexpr int BN = 128;
 constexpr int LDSP = BM + 4;  // padded LDS row (floats); multiple of 4 for b128 stores
 constexpr int NT = 256;
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Address of element (row r, k) of an operand whose layout is fixed at
 // compile time: KMAJOR 0 = element (r,k) at ptr[r*ld+k], 1 = at ptr[k*ld+r].
@@ -59,9 +63,6 @@ __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, i
 // Register staging of one BMxBK operand tile (NV4 float4 per thread).
 // KMAJOR == 0: thread -> (row tid/KQ + (NT/KQ) i, k 4*(tid%KQ) .. +3), KQ = BK/4
 // KMAJOR == 1: thread -> (k tid/32 + (NT/32) i, row 4*(tid%32) .. +3)
-// Direct products (input projection, dx) stage 16 k per tile: three
-// workgroups per CU.  Split-K weight gradients stage 32: half the barriers
-// and twice the MFMA work per load round (two workgroups per CU).
 constexpr int kDirectBK = 16;
 constexpr int kSplitBK = 32;
 static_assert(BM == 128 && BN == 128 && NT == 256, "tile staging layout");
@@ -109,11 +110,27 @@ __device__ __forceinline__ void load_tile(const GemmOperand& op, bool vec, int r
     }
 }
 
-template <int KMAJOR, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
+// LDS forms of an operand tile:
+//   row form ([row][k], row stride BK + 4): one ds_read_b128 gives a lane
+//     the values of four consecutive k of one row;
+//   k form   ([k][row], k stride LDSP): one ds_read_b128 gives four
+//     consecutive rows at one k.
+// A is kept in the form of its global layout (each float4 is written whole);
+// B always in k form, a row-major B being transposed on the way in.
+template <int LF, int BK>
+constexpr int lds_tile_floats() {
+    return LF == 0 ? BM * (BK + 4) : BK * LDSP;
+}
+
+template <int GK, int LF, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
 __device__ __forceinline__ void store_tile(float* lds, int tid, const float4 (&v)[NV4]) {
+    static_assert(!(GK == 1 && LF == 0), "k-major operands are staged in k form");
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
-        if constexpr (KMAJOR == 0) {
+        if constexpr (GK == 0 && LF == 0) {
+            const int r = tid / KQ + (NT / KQ) * i;
+            *reinterpret_cast<float4*>(lds + r * (BK + 4) + 4 * (tid % KQ)) = v[i];
+        } else if constexpr (GK == 0) {
             const int r = tid / KQ + (NT / KQ) * i;
             const int k = 4 * (tid % KQ);
             lds[(k + 0) * LDSP + r] = v[i].x;
@@ -122,8 +139,7 @@ __device__ __forceinline__ void store_tile(float* lds, int tid, const float4 (&v
             lds[(k + 3) * LDSP + r] = v[i].w;
         } else {
             const int k = tid / 32 + (NT / 32) * i;
-            const int r = 4 * (tid % 32);
-            *reinterpret_cast<float4*>(lds + k * LDSP + r) = v[i];
+            *reinterpret_cast<float4*>(lds + k * LDSP + 4 * (tid % 32)) = v[i];
         }
     }
 }
@@ -136,6 +152,7 @@ struct GemmArgs {
     const float* bias;     // direct mode
     float* c;              // direct mode output
     int ldc;
+    int c_vec;             // float4 stores of C / partials allowed
     float* partial;        // split mode: [ksplit][m][n] then colsum [ksplit][m]
     int want_colsum;
     int tiles_m, tiles;    // split mode: output tiles along m, in total
@@ -164,118 +181,91 @@ __device__ __forceinline__ void split_coords(const GemmArgs& p, int& bx, int& by
     by = tile / p.tiles_m;
 }
 
-// MFMAs of one k-tile from LDS (as, bs) into acc; the column sum of A (the
-// bias gradient) rides along for split-K products.
-template <int BK>
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l%16][k = l/16] and
+// B[k = l/16][l%16]; register r of D holds D[4 (l/16) + r][l%16].  A
+// wavefront computes 64x64 as 4x4 blocks.  Within a 16-deep k slab, lane
+// group g = l/16 takes k = 4 g + j at MFMA step j (the same assignment for
+// both operands, so every product term appears once).  Block rows:
+//   A in row form: block a, MFMA row i = tile row 16 a + i;
+//   A in k form:   block a, MFMA row i = tile row 4 i + a;
+//   B (k form):    block b, MFMA column c = tile column 4 c + b,
+// so a lane's four B blocks are four adjacent output columns (float4 stores).
+template <int ALF, int BK>
 __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int lane, int wm, int wn, int tid,
-                                         bool colsum, float& cs, floatx16 (&acc)[2][2]) {
+                                         bool colsum, float& cs, floatx4 (&acc)[4][4]) {
     if (colsum && tid < BM) {
+        // column sums of A (bias gradients of split-K products; A in k form)
 #pragma unroll
         for (int kk = 0; kk < BK; ++kk) cs += as[kk * LDSP + tid];
     }
-    // All operand fragments of the tile are read into distinct registers
-    // first: reusing one set per k-step would make every step's LDS reads
-    // wait for the previous step's MFMAs to consume their operands and
-    // leave the matrix core idle for an LDS latency each step.
-    constexpr int KS = BK / 2;
-    float fa0[KS], fa1[KS], fb0[KS], fb1[KS];
+    const int i = lane & 15, g = lane >> 4;
+    constexpr int NS = BK / 16;
+    // every operand fragment of the tile first (distinct registers), so the
+    // MFMAs of a slab do not wait on LDS reads issued behind earlier MFMAs
+    float4 fa[NS][4], fb[NS][4];
 #pragma unroll
-    for (int q = 0; q < KS; ++q) {
-        const int row = (2 * q + (lane >> 5)) * LDSP + (lane & 31);
-        fa0[q] = as[row + wm * 64];
-        fa1[q] = as[row + wm * 64 + 32];
-        fb0[q] = bs[row + wn * 64];
-        fb1[q] = bs[row + wn * 64 + 32];
+    for (int q = 0; q < NS; ++q) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            if constexpr (ALF == 0)
+                fa[q][x] = *reinterpret_cast<const float4*>(as + (wm * 64 + 16 * x + i) * (BK + 4) + 16 * q + 4 * g);
+            else
+                fa[q][x] = *reinterpret_cast<const float4*>(as + (16 * q + 4 * g + x) * LDSP + wm * 64 + 4 * i);
+            fb[q][x] = *reinterpret_cast<const float4*>(bs + (16 * q + 4 * g + x) * LDSP + wn * 64 + 4 * i);
+        }
     }
-    // keep the scheduler from sinking the reads back between the MFMAs
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < KS; ++q) {
-        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb0[q], acc[0][0], 0, 0, 0);
-        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[q], fb1[q], acc[0][1], 0, 0, 0);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb0[q], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[q], fb1[q], acc[1][1], 0, 0, 0);
-    }
-}
-
-// Interior tiles of vector-capable operands with a whole number of k-tiles
-// (the input projection at the GRU's shapes): operand tiles are
-// prefetched two k-tiles ahead into alternating register sets.  The loads of
-// tile kb+2 are issued before the MFMAs of tile kb and stored to LDS at the
-// end of iteration kb+1, so a load has two MFMA bursts (~1.7 us at BK 16) to
-// arrive.  Every iteration issues the same loads (past the last tile they
-// re-read it), so the wait before an LDS store covers exactly the older set.
-template <int AK, int BKM, bool BSHIFT, bool SEG, int BK>
-__device__ __forceinline__ void mainloop_fast(const GemmArgs& p, int m0, int n0, int kbeg, int nkb, int tid,
-                                              int lane, int wm, int wn, bool colsum, float& cs,
-                                              float (*As)[BK * LDSP], float (*Bs)[BK * LDSP],
-                                              floatx16 (&acc)[2][2]) {
-    constexpr int NV4 = BM * BK / (4 * NT);
-    constexpr int KQ = BK / 4;
-    // per-thread base addresses at k = kbeg; a k-tile advances them by a
-    // fixed stride (the row remap of SHIFT is recomputed per tile)
-    auto load = [&](float4 (&ra)[NV4], float4 (&rb)[NV4], int kb) {
-        const int k0 = kbeg + min(kb, nkb - 1) * BK;
+    for (int q = 0; q < NS; ++q) {
 #pragma unroll
-        for (int i = 0; i < NV4; ++i) {
-            const int ra_r = AK == 0 ? m0 + tid / KQ + (NT / KQ) * i : m0 + 4 * (tid % 32);
-            const int ra_k = AK == 0 ? k0 + 4 * (tid % KQ) : k0 + tid / 32 + (NT / 32) * i;
-            ra[i] = *reinterpret_cast<const float4*>(elem_ptr<AK, false, SEG>(p.a, ra_r, ra_k));
-            const int rb_r = BKM == 0 ? n0 + tid / KQ + (NT / KQ) * i : n0 + 4 * (tid % 32);
-            const int rb_k = BKM == 0 ? k0 + 4 * (tid % KQ) : k0 + tid / 32 + (NT / 32) * i;
-            rb[i] = *reinterpret_cast<const float4*>(elem_ptr<BKM, BSHIFT, SEG>(p.b, rb_r, rb_k));
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                // row form: fa[q][block a] holds steps 0..3; k form: fa[q][step j] holds blocks 0..3
+                const float av = ALF == 0 ? fa[q][a][j] : fa[q][j][a];
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, fb[q][j][b], acc[a][b], 0, 0, 0);
+            }
         }
-    };
-    float4 ra0[NV4], rb0[NV4], ra1[NV4], rb1[NV4];
-    auto step = [&](int kb, int cur, float4 (&fa)[NV4], float4 (&fb)[NV4], float4 (&na)[NV4],
-                    float4 (&nb)[NV4]) {
-        load(fa, fb, kb + 2);
-        mma_tile<BK>(As[cur], Bs[cur], lane, wm, wn, tid, colsum, cs, acc);
-        if (kb + 1 < nkb) {
-            store_tile<AK, BK>(As[cur ^ 1], tid, na);
-            store_tile<BKM, BK>(Bs[cur ^ 1], tid, nb);
-        }
-        __syncthreads();
-    };
-    load(ra0, rb0, 0);
-    load(ra1, rb1, 1);
-    store_tile<AK, BK>(As[0], tid, ra0);
-    store_tile<BKM, BK>(Bs[0], tid, rb0);
-    __syncthreads();
-    for (int kb = 0; kb < nkb; kb += 2) {
-        step(kb, 0, ra0, rb0, ra1, rb1);
-        if (kb + 1 < nkb) step(kb + 1, 1, ra1, rb1, ra0, rb0);
     }
 }
 
-// Any tile (edges, unaligned or odd-extent operands): one tile of register
-// prefetch, per-element bounds where needed.
+// The k loop: the next k-tile is loaded into registers while the MFMAs of
+// the current one run, then stored to the other LDS buffer; one barrier per
+// k-tile.  Interior tiles of vector-capable operands load float4 without
+// bounds checks; edge tiles check per element.  (A two-deep register
+// prefetch measured slower at c2: its registers cost a resident workgroup
+// per CU.)
 template <int AK, int BKM, bool BSHIFT, bool SEG, int BK>
-__device__ __forceinline__ void mainloop_general(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int nkb,
+__device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int nkb,
                                                  int tid, int lane, int wm, int wn, bool colsum, float& cs,
-                                                 float (*As)[BK * LDSP], float (*Bs)[BK * LDSP],
-                                                 floatx16 (&acc)[2][2]) {
+                                                 float* As0, float* As1, float* Bs0, float* Bs1,
+                                                 floatx4 (&acc)[4][4]) {
     constexpr int NV4 = BM * BK / (4 * NT);
     const bool av = p.a_vec != 0, bv = p.b_vec != 0;
     float4 ra[NV4], rb[NV4];
     if (nkb > 0) {
         load_tile<AK, false, SEG, BK>(p.a, av, p.m, kend, m0, kbeg, tid, ra);
         load_tile<BKM, BSHIFT, SEG, BK>(p.b, bv, p.n, kend, n0, kbeg, tid, rb);
-        store_tile<AK, BK>(As[0], tid, ra);
-        store_tile<BKM, BK>(Bs[0], tid, rb);
+        store_tile<AK, AK, BK>(As0, tid, ra);
+        store_tile<BKM, 1, BK>(Bs0, tid, rb);
     }
     __syncthreads();
     for (int kb = 0; kb < nkb; ++kb) {
-        const int cur = kb & 1;
+        float* as = (kb & 1) ? As1 : As0;
+        float* bs = (kb & 1) ? Bs1 : Bs0;
+        float* as_n = (kb & 1) ? As0 : As1;
+        float* bs_n = (kb & 1) ? Bs0 : Bs1;
         const bool more = kb + 1 < nkb;
         if (more) {
             load_tile<AK, false, SEG, BK>(p.a, av, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
             load_tile<BKM, BSHIFT, SEG, BK>(p.b, bv, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
         }
-        mma_tile<BK>(As[cur], Bs[cur], lane, wm, wn, tid, colsum, cs, acc);
+        mma_tile<AK, BK>(as, bs, lane, wm, wn, tid, colsum, cs, acc);
         if (more) {
-            store_tile<AK, BK>(As[cur ^ 1], tid, ra);
-            store_tile<BKM, BK>(Bs[cur ^ 1], tid, rb);
+            store_tile<AK, AK, BK>(as_n, tid, ra);
+            store_tile<BKM, 1, BK>(bs_n, tid, rb);
         }
         __syncthreads();
     }
@@ -283,8 +273,13 @@ __device__ __forceinline__ void mainloop_general(const GemmArgs& p, int m0, int 
 
 template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
-    __shared__ __attribute__((aligned(16))) float As[2][BK * LDSP];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDSP];
+    constexpr int AF = lds_tile_floats<AK, BK>();
+    constexpr int BF = lds_tile_floats<1, BK>();
+    __shared__ __attribute__((aligned(16))) float smem[2 * AF + 2 * BF];
+    float* As0 = smem;
+    float* As1 = smem + AF;
+    float* Bs0 = smem + 2 * AF;
+    float* Bs1 = smem + 2 * AF + BF;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -299,52 +294,56 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     const int nkb = (kend - kbeg + BK - 1) / BK;
     const bool colsum = SPLIT && p.want_colsum && by == 0;
 
-    floatx16 acc[2][2];
+    floatx4 acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
     float cs = 0.f;
 
-    // The two-deep prefetch pays for the input projection (row-major A and
-    // B: 141 vs 145 us at c2) but not for dx (166 vs 137 us) or the split-K
-    // products (257 vs 166 us): its registers cut the resident workgroups
-    // per CU from three to two (one for split-K), so only that layout uses it.
-    constexpr bool kFastLayout = !SPLIT && AK == 0 && BKM == 0;
-    const bool fast = kFastLayout && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 &&
-                      (kend - kbeg) % BK == 0;
-    if constexpr (kFastLayout) {
-        if (fast) {
-            mainloop_fast<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, As, Bs,
-                                                    acc);
-        } else {
-            mainloop_general<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs,
-                                                       As, Bs, acc);
-        }
-    } else
-        mainloop_general<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As,
-                                                   Bs, acc);
+    mainloop<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
+                                       Bs1, acc);
 
-    // Output layout of a 32x32 MFMA block: lane l, register r holds
-    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    // Epilogue: acc[a][b][r] is C(row(a, 4 g + r), n0 + 64 wn + 4 c + b); a
+    // lane's four b values are one float4 of a C row.
+    const int c = lane & 15, g = lane >> 4;
+    const int n = n0 + wn * 64 + 4 * c;
+    float4 bias4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!SPLIT && p.bias) {
+        if (n + 3 < p.n) {
+            bias4 = make_float4(p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]);
+        } else {
+            bias4.x = n < p.n ? p.bias[n] : 0.f;
+            bias4.y = n + 1 < p.n ? p.bias[n + 1] : 0.f;
+            bias4.z = n + 2 < p.n ? p.bias[n + 2] : 0.f;
+        }
+    }
+    const bool vec_store = p.c_vec && n + 3 < p.n;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int a = 0; a < 4; ++a) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (n >= p.n) continue;
-            const float bias = (!SPLIT && p.bias) ? p.bias[n] : 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m >= p.m) continue;
-                if (SPLIT) {
-                    p.partial[((size_t)(p.z_off + bz) * p.m + m) * p.n + n] = acc[i][j][r];
-                } else {
-                    p.c[(size_t)seg_map<SEG>(p.c_seg, m) * p.ldc + n] = acc[i][j][r] + bias;
-                }
+        for (int r = 0; r < 4; ++r) {
+            const int lr = 4 * g + r;  // MFMA row within block a
+            const int m = m0 + wm * 64 + (AK == 0 ? 16 * a + lr : 4 * lr + a);
+            if (m >= p.m || n >= p.n) continue;
+            float4 v = make_float4(acc[a][0][r], acc[a][1][r], acc[a][2][r], acc[a][3][r]);
+            float* dst;
+            if (SPLIT) {
+                dst = p.partial + ((size_t)(p.z_off + bz) * p.m + m) * p.n + n;
+            } else {
+                v.x += bias4.x;
+                v.y += bias4.y;
+                v.z += bias4.z;
+                v.w += bias4.w;
+                dst = p.c + (size_t)seg_map<SEG>(p.c_seg, m) * p.ldc + n;
+            }
+            if (vec_store) {
+                *reinterpret_cast<float4*>(dst) = v;
+            } else {
+                dst[0] = v.x;
+                if (n + 1 < p.n) dst[1] = v.y;
+                if (n + 2 < p.n) dst[2] = v.z;
+                if (n + 3 < p.n) dst[3] = v.w;
             }
         }
     }
@@ -451,6 +450,7 @@ int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
     args.bias = bias;
     args.c = c;
     args.ldc = ldc;
+    args.c_vec = (ldc % 4 == 0 && aligned16(c)) ? 1 : 0;
     args.c_seg = c_seg;
     return launch_gemm<false>(args, 1, vec_ok(a, m, k), vec_ok(b, n, k), stream);
 }
@@ -485,6 +485,7 @@ int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOp
     const int kper = (k + ksplit - 1) / ksplit;
     args.kchunk = (kper + kSplitBK - 1) / kSplitBK * kSplitBK;
     args.partial = partial;
+    args.c_vec = (n % 4 == 0 && aligned16(partial)) ? 1 : 0;
     args.want_colsum = want_colsum ? 1 : 0;
     args.z_off = z_off;
     args.ksplit_total = ksplit_total;

@@ -13,7 +13,7 @@ namespace rka {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxReduceBlocks = 1024;   // partial sums of a loss reduction
+constexpr int kMaxReduceBlocks = 2048;   // partial sums of a loss reduction
 constexpr int kHeadBlocks = 512;         // row ranges of the head's dw reduction
 
 // Sum over the block's threads in a fixed tree order; the result is valid in
@@ -31,17 +31,42 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
 
 // ------------------------------------------------------------------ MSE ---
 // Block b sums (pred - target)^2 over its contiguous range of `chunk`
-// elements (thread t: elements t, t + 256, ... of the range).
+// elements.  Vector form (chunk a multiple of 4, both operands 16-byte
+// aligned): thread t takes float4 t, t + 256, ... of the range into four
+// running sums (one per component), combined as (s0 + s1) + (s2 + s3);
+// scalar form: elements t, t + 256, ... into one sum.
 __global__ __launch_bounds__(kThreads) void mse_partial_kernel(const float* __restrict__ pred,
                                                                const float* __restrict__ target, size_t n,
-                                                               size_t chunk, float* __restrict__ partial) {
+                                                               size_t chunk, int vec, float* __restrict__ partial) {
     __shared__ float scratch[kThreads];
     const size_t beg = (size_t)blockIdx.x * chunk;
     const size_t end = beg + chunk < n ? beg + chunk : n;
     float acc = 0.f;
-    for (size_t i = beg + threadIdx.x; i < end; i += kThreads) {
-        const float d = pred[i] - target[i];
-        acc = fmaf(d, d, acc);
+    if (vec) {
+        const float4* p4 = reinterpret_cast<const float4*>(pred + beg);
+        const float4* t4 = reinterpret_cast<const float4*>(target + beg);
+        const size_t n4 = (end - beg) / 4;
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll 4
+        for (size_t i = threadIdx.x; i < n4; i += kThreads) {
+            const float4 a = p4[i], b = t4[i];
+            const float dx = a.x - b.x, dy = a.y - b.y, dz = a.z - b.z, dw = a.w - b.w;
+            s0 = fmaf(dx, dx, s0);
+            s1 = fmaf(dy, dy, s1);
+            s2 = fmaf(dz, dz, s2);
+            s3 = fmaf(dw, dw, s3);
+        }
+        // the last range may end inside a float4
+        for (size_t i = beg + 4 * n4 + threadIdx.x; i < end; i += kThreads) {
+            const float d = pred[i] - target[i];
+            s0 = fmaf(d, d, s0);
+        }
+        acc = (s0 + s1) + (s2 + s3);
+    } else {
+        for (size_t i = beg + threadIdx.x; i < end; i += kThreads) {
+            const float d = pred[i] - target[i];
+            acc = fmaf(d, d, acc);
+        }
     }
     const float s = block_sum(acc, scratch);
     if (threadIdx.x == 0) partial[blockIdx.x] = s;
@@ -59,22 +84,40 @@ __global__ __launch_bounds__(kThreads) void mse_finish_kernel(const float* __res
 }
 
 // grad_pred = grad_loss * 2 (pred - target) / n  (torch's mse_loss backward
-// for reduction='mean': norm = 2 / n, grad = norm * (pred - target) * grad)
+// for reduction='mean': norm = 2 / n, grad = norm * (pred - target) * grad);
+// float4 per thread when all three arrays are 16-byte aligned.
 __global__ __launch_bounds__(kThreads) void mse_backward_kernel(const float* __restrict__ pred,
                                                                 const float* __restrict__ target,
                                                                 const float* __restrict__ grad_loss, size_t n,
-                                                                float* __restrict__ grad_pred) {
+                                                                int vec, float* __restrict__ grad_pred) {
     const float norm = 2.0f / (float)n;
     const float g = grad_loss[0];
-    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (size_t)gridDim.x * kThreads)
+    const size_t stride = (size_t)gridDim.x * kThreads;
+    size_t first = 0;
+    if (vec) {
+        const size_t n4 = n / 4;
+        const float4* p4 = reinterpret_cast<const float4*>(pred);
+        const float4* t4 = reinterpret_cast<const float4*>(target);
+        float4* g4 = reinterpret_cast<float4*>(grad_pred);
+        for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
+            const float4 a = p4[i], b = t4[i];
+            g4[i] = make_float4(norm * (a.x - b.x) * g, norm * (a.y - b.y) * g, norm * (a.z - b.z) * g,
+                                norm * (a.w - b.w) * g);
+        }
+        first = 4 * n4;
+    }
+    for (size_t i = first + (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
         grad_pred[i] = norm * (pred[i] - target[i]) * g;
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Blocks of the loss reduction and the range of each (a multiple of 4).
 int mse_blocks(size_t n, size_t* chunk) {
     const size_t nb = std::min<size_t>(kMaxReduceBlocks, (n + 4095) / 4096);
     const size_t b = nb < 1 ? 1 : nb;
-    *chunk = (n + b - 1) / b;
-    return (int)b;
+    *chunk = ((n + b - 1) / b + 3) / 4 * 4;
+    return (int)((n + *chunk - 1) / *chunk);
 }
 
 // ----------------------------------------------------------------- head ---
@@ -208,7 +251,8 @@ int rka_mse_forward(const float* pred, const float* target, float* loss, void* w
         return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "mse_forward: workspace too small");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     float* partial = reinterpret_cast<float*>(workspace);
-    hipLaunchKernelGGL(mse_partial_kernel, dim3(nb), dim3(kThreads), 0, s, pred, target, n, chunk, partial);
+    const int vec = (aligned16(pred) && aligned16(target)) ? 1 : 0;
+    hipLaunchKernelGGL(mse_partial_kernel, dim3(nb), dim3(kThreads), 0, s, pred, target, n, chunk, vec, partial);
     RKA_RETURN_IF_HIP(hipGetLastError());
     hipLaunchKernelGGL(mse_finish_kernel, dim3(1), dim3(kThreads), 0, s, partial, nb, n, loss);
     RKA_RETURN_IF_HIP(hipGetLastError());
@@ -219,9 +263,10 @@ int rka_mse_backward(const float* pred, const float* target, const float* grad_l
                      void* stream) {
     if (n == 0 || !pred || !target || !grad_loss || !grad_pred)
         return fail(RKA_ERR_INVALID_ARGUMENT, "mse_backward: bad arguments");
-    const size_t blocks = std::min<size_t>((n + kThreads - 1) / kThreads, 4096);
-    hipLaunchKernelGGL(mse_backward_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
-                       reinterpret_cast<hipStream_t>(stream), pred, target, grad_loss, n, grad_pred);
+    const int vec = (aligned16(pred) && aligned16(target) && aligned16(grad_pred)) ? 1 : 0;
+    const size_t blocks = std::min<size_t>((n / (vec ? 4 : 1) + kThreads - 1) / kThreads, 4096);
+    hipLaunchKernelGGL(mse_backward_kernel, dim3((unsigned)std::max<size_t>(blocks, 1)), dim3(kThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), pred, target, grad_loss, n, vec, grad_pred);
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
 }
