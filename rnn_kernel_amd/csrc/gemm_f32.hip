@@ -73,6 +73,27 @@ __device__ __forceinline__ void load_tile(const GemmOperand& op, bool vec, int r
     if (vec && r0 + BM <= rows && k0 + BK <= kend) {
         // interior tile of a vector-capable operand (the common case; the
         // test is uniform): no per-lane bounds checks
+        if constexpr (KMAJOR == 1 && SHIFT && !SEG) {
+            // the [h0 ; y[:, :-1]] remap with one division per tile: the
+            // thread's rows k, k + NT/32, ... advance t and wrap into the next
+            // sequence at t == T
+            const int kk = k0 + tid / 32;
+            const int r = r0 + 4 * (tid % 32);
+            int b = kk / op.shift_T;
+            int t = kk - b * op.shift_T;
+#pragma unroll
+            for (int i = 0; i < NV4; ++i) {
+                const float* src = t == 0 ? op.shift_first + (size_t)b * op.ld + r
+                                          : op.ptr + (size_t)(kk + (NT / 32) * i - 1) * op.ld + r;
+                v[i] = *reinterpret_cast<const float4*>(src);
+                t += NT / 32;
+                while (t >= op.shift_T) {
+                    t -= op.shift_T;
+                    ++b;
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < NV4; ++i) {
             const int r = KMAJOR == 0 ? r0 + tid / KQ + (NT / KQ) * i : r0 + 4 * (tid % 32);
@@ -353,22 +374,41 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     }
 }
 
-// out[o*ldc + n] = sum_z partial[z][(o+rot)%m][n]; colsum likewise.
+// out[o*ldc + n] = sum_z partial[z][(o+rot)%m][n] (z in order); colsum
+// likewise.  With vec, a thread sums one float4 of a row.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int ksplit,
                                                             int m, int n, int rot, float* __restrict__ c,
-                                                            int ldc, float* __restrict__ colsum) {
-    const size_t total = (size_t)m * n + (colsum ? m : 0);
+                                                            int ldc, float* __restrict__ colsum, int vec) {
+    const size_t per_row = vec ? (size_t)(n / 4) : (size_t)n;
+    const size_t items = (size_t)m * per_row;
+    const size_t total = items + (colsum ? m : 0);
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (size_t)gridDim.x * blockDim.x) {
-        if (idx < (size_t)m * n) {
-            const int o = (int)(idx / n);
-            const int col = (int)(idx % n);
+        if (idx < items) {
+            const int o = (int)(idx / per_row);
             const int src = rot ? (o + rot) % m : o;
-            float s = 0.f;
-            for (int z = 0; z < ksplit; ++z) s += partial[((size_t)z * m + src) * n + col];
-            c[(size_t)o * ldc + col] = s;
+            if (vec) {
+                const int col = 4 * (int)(idx % per_row);
+                const float* pp = partial + (size_t)src * n + col;
+                float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+                for (int z = 0; z < ksplit; ++z) {
+                    const float4 v = *reinterpret_cast<const float4*>(pp + (size_t)z * m * n);
+                    s.x += v.x;
+                    s.y += v.y;
+                    s.z += v.z;
+                    s.w += v.w;
+                }
+                *reinterpret_cast<float4*>(c + (size_t)o * ldc + col) = s;
+            } else {
+                const int col = (int)(idx % per_row);
+                float s = 0.f;
+#pragma unroll 8
+                for (int z = 0; z < ksplit; ++z) s += partial[((size_t)z * m + src) * n + col];
+                c[(size_t)o * ldc + col] = s;
+            }
         } else {
-            const int o = (int)(idx - (size_t)m * n);
+            const int o = (int)(idx - items);
             const int src = rot ? (o + rot) % m : o;
             const float* cpart = partial + (size_t)ksplit * m * n;
             float s = 0.f;
@@ -494,10 +534,11 @@ int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOp
 
 int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,
                   float* colsum, hipStream_t stream) {
-    const size_t total = (size_t)m * n + (colsum ? m : 0);
+    const int vec = (n % 4 == 0 && ldc % 4 == 0 && aligned16(partial) && aligned16(c)) ? 1 : 0;
+    const size_t total = (size_t)m * (vec ? n / 4 : n) + (colsum ? m : 0);
     const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, ksplit_total, m, n,
-                       rot, c, ldc, colsum);
+                       rot, c, ldc, colsum, vec);
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
 }
