@@ -329,19 +329,6 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
     }
 }
 
-// Row-broadcast FMAs over lanes K0 .. K1-1 of each 16-lane row of src (see
-// dot16x3), with weights w?[K - K0].
-template <int K0, int K1, int K = K0>
-__device__ __forceinline__ void dot_range3(float (&ar)[2], float (&az)[2], float (&an)[2], float src,
-                                           const float* wr, const float* wz, const float* wn) {
-    if constexpr (K < K1) {
-        rec::fma_row_bcast<K>(ar[K & 1], src, wr[K - K0]);
-        rec::fma_row_bcast<K>(az[K & 1], src, wz[K - K0]);
-        rec::fma_row_bcast<K>(an[K & 1], src, wn[K - K0]);
-        dot_range3<K0, K1, K + 1>(ar, az, an, src, wr, wz, wn);
-    }
-}
-
 // Forward recurrence for one batch row per workgroup at 193 <= H <= 256
 // (four slices) with the workgroup's own slice of h_{t-1} taken from LDS.
 // Wavefront w holds, for each slot j (slot 0 = its own slice, slots 1..3 =
@@ -350,14 +337,19 @@ __device__ __forceinline__ void dot_range3(float (&ar)[2], float (&az)[2], float
 // it to LDS; a second barrier follows and every wavefront runs the own
 // slot's 24 FMAs of step t+1 while the other slices' words are still on
 // their way, leaving 72 FMAs per lane after they arrive (96 with the whole
-// chunk polled).
+// chunk polled).  The h values reach the FMAs as wave-uniform VGPRs read
+// from LDS (broadcast ds_read_b128): the polled words are written to a
+// wave-private LDS row first.  Measured on MI355X, a VGPR-operand v_fmac_f32
+// issues at ~1.2 ns per SIMD with two waves per SIMD against ~2.0 ns for
+// the row-broadcast DPP form and ~2.1 ns with an SGPR operand.
 __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
     const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
     float* __restrict__ reserve, unsigned long long* __restrict__ exch, int* __restrict__ abort_flag,
     RegParams p) {
     __shared__ float part[2][NW][3][64];
-    __shared__ float hloc[2][64];
+    __shared__ __attribute__((aligned(16))) float hloc[2][64];
+    __shared__ __attribute__((aligned(16))) float hrem[NW][32];  // per wave: its 24 polled h values
     __shared__ int s_abort;
 
     const int B = p.B, T = p.T, H = p.H;
@@ -456,16 +448,36 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     };
     // partial sums of the step in flight; the own slot's FMAs land first
     float ar[2], az[2], an[2];
-    auto local_fmas = [&](float hl) {
+    // slot j's FMAs with its eight h values (wave-uniform)
+    auto fma8 = [&](const float (&hv)[8], int j) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ar[i & 1] = fmaf(hv[i], wr[8 * j + i], ar[i & 1]);
+            az[i & 1] = fmaf(hv[i], wz[8 * j + i], az[i & 1]);
+            an[i & 1] = fmaf(hv[i], wn[8 * j + i], an[i & 1]);
+        }
+    };
+    auto local_fmas = [&](const float (&hv)[8]) {
         ar[0] = ar[1] = az[0] = az[1] = an[0] = an[1] = 0.f;
-        rec::dpp_src_guard(hl);
-        dot_range3<0, 8>(ar, az, an, hl, wr, wz, wn);
+        fma8(hv, 0);
+    };
+    // eight consecutive floats of LDS as wave-uniform values
+    auto lds8 = [](const float* src, float (&hv)[8]) {
+        const float4 a = *reinterpret_cast<const float4*>(src);
+        const float4 b = *reinterpret_cast<const float4*>(src + 4);
+        hv[0] = a.x; hv[1] = a.y; hv[2] = a.z; hv[3] = a.w;
+        hv[4] = b.x; hv[5] = b.y; hv[6] = b.z; hv[7] = b.w;
     };
     unsigned long long first_read = 0;
-    // step 0's own slot from h0 (lane K of each row: k = kof(0, K))
+    // step 0's own slot from h0
     {
-        const int k = kof(0, lane & 7);
-        local_fmas(k < H ? h0[(size_t)row * H + k] : 0.f);
+        float hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int k = kof(0, i);
+            hv[i] = k < H ? h0[(size_t)row * H + k] : 0.f;
+        }
+        local_fmas(hv);
     }
     auto step = [&](int t, const float (&cur)[3], float (&nxt)[3]) -> bool {
         // @probe:step_begin
@@ -482,18 +494,23 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
             hx = pvalid ? __uint_as_float((unsigned)w[0]) : 0.f;
             if (!ok) s_abort = 1;
         }
-        float rows[4];
-        rec::rows_of(hx, rows);
+        // lanes 0..23 hold slot 1 + l / 8, entry l % 8: through the wave's
+        // LDS row to every lane (one wave writes and reads the row; LDS
+        // keeps a wave's accesses in order)
+        if (lane < 24) hrem[wave][lane] = hx;
+        __builtin_amdgcn_wave_barrier();
+        float hv1[8], hv2[8], hv3[8];
+        lds8(&hrem[wave][0], hv1);
+        lds8(&hrem[wave][8], hv2);
+        lds8(&hrem[wave][16], hv3);
         if (owner) {
             if (t > 0) store_outputs(t - 1);
             if (t + 1 < T) load_gx(nxt, t + 1);
         }
         // @probe:polled
-        rec::dpp_src_guard(rows[0]);
-        rec::dpp_src_guard(rows[1]);
-        dot_range3<0, 8>(ar, az, an, rows[0], wr + 8, wz + 8, wn + 8);
-        dot_range3<8, 16>(ar, az, an, rows[0], wr + 16, wz + 16, wn + 16);
-        dot_range3<0, 8>(ar, az, an, rows[1], wr + 24, wz + 24, wn + 24);
+        fma8(hv1, 1);
+        fma8(hv2, 2);
+        fma8(hv3, 3);
         part[t & 1][wave][0][lane] = ar[0] + ar[1];
         part[t & 1][wave][1][lane] = az[0] + az[1];
         part[t & 1][wave][2][lane] = an[0] + an[1];
@@ -526,7 +543,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         // with the first poll read of step t+1 already in flight
         if (t + 1 < T) {
             first_read = rec::load_word(exch + (size_t)(t & 1) * B * H + (size_t)row * H + pidx);
-            local_fmas(hloc[t & 1][8 * wave + (lane & 7)]);
+            float hv[8];
+            lds8(&hloc[t & 1][8 * wave], hv);
+            local_fmas(hv);
         }
         // @probe:step_end
         return !abort_now;
