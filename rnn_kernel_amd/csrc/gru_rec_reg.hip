@@ -745,32 +745,42 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
     if (owner) dh0[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : dh;
 }
 
-//   acc[K & 7] += src(lane K of the row) * w[K - K0], K = K0 .. K1-1
-template <int K0, int K1, int K = K0>
-__device__ __forceinline__ void dot_range1(float (&acc)[8], float src, const float* w) {
-    if constexpr (K < K1) {
-        rec::fma_row_bcast<K>(acc[K & 7], src, w[K - K0]);
-        dot_range1<K0, K1, K + 1>(acc, src, w);
-    }
+// Sum of x over the four 16-lane rows, in every row: (X0 + X2) + (X1 + X3).
+__device__ __forceinline__ float rows_total(float x) {
+    const unsigned ux = __float_as_uint(x);
+    const auto a = __builtin_amdgcn_permlane32_swap(ux, ux, false, false);  // (X0 X1 X0 X1), (X2 X3 X2 X3)
+    const float sum = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const unsigned us = __float_as_uint(sum);
+    const auto b = __builtin_amdgcn_permlane16_swap(us, us, false, false);  // (S0 S0 S2 S2), (S1 S1 S3 S3)
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Backward recurrence for one batch row per workgroup at 193 <= H <= 256
-// (four slices) with the workgroup's own G_h words taken from LDS.  The 192
-// words of a slice (gate c, unit m at index 64 c + m) are dealt 24 per
-// wavefront: wavefront w holds, for slot j (0 = own slice, 1..3 = the others
-// in rotation), entries e < 24 of index 24 w + e, i.e. W_hh column u at
-// row c H + 64 ((s + j) mod 4) + m.  At the end of a step the owner
-// reduces dh, runs the next step's pointwise math, publishes its G words and
-// writes them to LDS; after a second barrier every wavefront runs the own
-// slot's 24 FMAs while the other slices' words travel, leaving 72 after
-// they arrive (96 with the whole chunk polled).
+// (four slices) with the workgroup's own G_h words taken from LDS.
+// The 3H G_h words of a step are split into the workgroup's own 192 (gate
+// c, unit m of its slice at index e = 64 c + m) and 576 remote ones (flat
+// index r: slot 1 + r / 192 of the other slices in rotation, then e).  The
+// workgroup's 32 sixteen-lane rows are j-groups: row J = 4 w + rho of wave w
+// takes own entries 6 J .. 6 J + 5 and remote entries 18 J .. 18 J + 17, and
+// lane q of the row takes units 64 s + 4 q .. 4 q + 3, so every G value
+// feeds four FMAs of a lane.  The G values reach the FMAs as VGPRs uniform
+// over a row (ds_read_b128 from LDS, one address per row): plain v_fmac_f32
+// issues at ~1.2 ns per SIMD with two waves per SIMD on MI355X against
+// ~2.0 ns for the row-broadcast DPP form, and with four FMAs per value the
+// broadcast reads (1 KB per instruction) stay within LDS bandwidth.  Row
+// partials are summed across the wave's rows with permlane swaps, then
+// across the 8 waves in LDS.  At the end of a step the owner reduces dh,
+// runs the next step's pointwise math, publishes its G words and writes
+// them to LDS; after a second barrier every wave runs the own entries' FMAs
+// while the other slices' words travel.
 __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
     const float* __restrict__ h0, const float* __restrict__ y, const float* __restrict__ w_hh,
     float* __restrict__ gout, float* __restrict__ dh0, unsigned long long* __restrict__ exch,
     int* __restrict__ abort_flag, RegParams p) {
-    __shared__ float part[2][NW][64];
-    __shared__ float gloc[192];
+    __shared__ __attribute__((aligned(16))) float part[2][NW][64];
+    __shared__ __attribute__((aligned(16))) float gloc[32][8];      // own G words by j-group (6 used)
+    __shared__ __attribute__((aligned(16))) float grem[NW][4][20];  // per wave: polled words by row (18 used)
     __shared__ int s_abort;
 
     const int B = p.B, T = p.T, H = p.H;
@@ -779,25 +789,51 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     const int wave = threadIdx.x >> 6;
     const int row = blockIdx.x % p.G;
     const int s = blockIdx.x / p.G;
-    const int u = s * 64 + lane;
+    const int u = s * 64 + lane;  // the owner lane's unit
     const bool uvalid = u < H;
-    // W_hh row of entry e of slot j; valid = the unit exists
-    auto jof = [&](int j, int e, bool& valid) {
-        const int idx = 24 * wave + e;
-        const int unit = 64 * ((s + j) & 3) + (idx & 63);
-        valid = unit < H;
-        return (idx >> 6) * H + unit;
+    const int rho = lane >> 4, q = lane & 15;
+    const int J = 4 * wave + rho;
+    const int ub = s * 64 + 4 * q;  // the lane's first FMA unit
+    // W_hh row of own entry e / remote entry r; valid = the unit exists
+    auto own_row = [&](int e, bool& valid) {
+        const int m = e & 63;
+        valid = 64 * s + m < H;
+        return (e >> 6) * H + 64 * s + m;
+    };
+    auto rem_row = [&](int r, bool& valid) {
+        const int e = r % 192, m = e & 63, sl = (s + 1 + r / 192) & 3;
+        valid = 64 * sl + m < H;
+        return (e >> 6) * H + 64 * sl + m;
     };
 
-    float w[96];
+    // W_hh[j][ub .. ub + 3] for the row's own (wl) and remote (wm) entries
+    float wl[6][4], wm[18][4];
+    const bool vec = p.wvec != 0;
+    auto load4 = [&](int jr, bool ok, float (&d)[4]) {
+        const float* src = w_hh + (size_t)jr * H + ub;
+        if (vec) {
+            const float4 v = (ok && ub < H) ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+            d[0] = v.x;
+            d[1] = v.y;
+            d[2] = v.z;
+            d[3] = v.w;
+        } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 24; ++e) {
-            bool ok;
-            const int jr = jof(j, e, ok);
-            w[24 * j + e] = (ok && uvalid) ? w_hh[(size_t)jr * H + u] : 0.f;
+            for (int v = 0; v < 4; ++v) d[v] = (ok && ub + v < H) ? src[v] : 0.f;
         }
+    };
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        bool ok;
+        const int jr = own_row(6 * J + i, ok);
+        load4(jr, ok, wl[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 18; ++i) {
+        bool ok;
+        const int jr = rem_row(18 * J + i, ok);
+        load4(jr, ok, wm[i]);
+    }
 
     const bool owner = wave == 0 && uvalid;
     float dh = 0.f, ddirect = 0.f;
@@ -827,28 +863,29 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     __shared__ int s_local;
     const bool xlocal = rec::group_on_one_xcd(p.xcc_words, row, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
 
-    // Poll register 0: lane l reads remote entry l (slot 1 + l / 24, entry
-    // l % 24); register 1: lane l reads remote entry 64 + l % 8.  Lanes
-    // without a word re-read the register's first valid word (else the
-    // wave's first valid remote word, else word 0).
+    // Wave w polls remote entries 72 w .. 72 w + 71: register 0 lane l entry
+    // 72 w + l, register 1 lane l entry 72 w + 64 + l % 8.  Lanes without a
+    // word re-read the register's first valid word (else the wave's first
+    // valid remote word, else word 0).
     int first_any = -1, first1 = -1;
 #pragma unroll
-    for (int r = 0; r < 72; ++r) {
+    for (int e = 0; e < 72; ++e) {
         bool ok;
-        const int jr = jof(1 + r / 24, r % 24, ok);
+        const int jr = rem_row(72 * wave + e, ok);
         if (ok && first_any < 0) first_any = jr;
-        if (ok && r >= 64 && first1 < 0) first1 = jr;
+        if (ok && e >= 64 && first1 < 0) first1 = jr;
     }
     if (first_any < 0) first_any = 0;
     if (first1 < 0) first1 = first_any;
     bool pv0, pv1;
-    int pidx0 = jof(1 + lane / 24, lane % 24, pv0);
-    int pidx1 = jof(3, 16 + (lane & 7), pv1);
+    int pidx0 = rem_row(72 * wave + lane, pv0);
+    int pidx1 = rem_row(72 * wave + 64 + (lane & 7), pv1);
     if (!pv0) pidx0 = first_any;
     if (!pv1) pidx1 = first1;
 
     // pointwise step i (t = T-1-i) from dh and its inputs: publishes G_h,t,
-    // keeps the gate gradients for the store after the next poll
+    // writes it to LDS by j-group, keeps the gate gradients for the store
+    // after the next poll
     auto pointwise = [&](int i, const float (&cur)[6]) {
         if (owner) {
             const float gsum = dh + cur[0];
@@ -867,31 +904,39 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
             rec::publish_words<3>(pp3, w3, xlocal);
         }
         if (wave == 0) {
-            gloc[lane] = owner ? o_drh : 0.f;
-            gloc[64 + lane] = owner ? o_dzh : 0.f;
-            gloc[128 + lane] = owner ? o_dan : 0.f;
+            const float gv[3] = {owner ? o_drh : 0.f, owner ? o_dzh : 0.f, owner ? o_dan : 0.f};
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const int e = 64 * c + lane;
+                gloc[e / 6][e % 6] = gv[c];
+            }
         }
     };
-    float acc[8];
-    // the first poll reads of step i, issued ahead of its own-slot FMAs
+    float acc[2][4];
+    // FMAs of the row's n values g[0 .. n-1] with the weights wt
+    auto fma_group = [&](const float* g, int n, const float (*wt)[4]) {
+#pragma unroll
+        for (int i = 0; i < n; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[i & 1][v] = fmaf(g[i], wt[i][v], acc[i & 1][v]);
+    };
+    auto local_fmas = [&]() {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[0][v] = acc[1][v] = 0.f;
+        const float4 a = *reinterpret_cast<const float4*>(&gloc[J][0]);
+        const float4 b = *reinterpret_cast<const float4*>(&gloc[J][4]);
+        const float g[6] = {a.x, a.y, a.z, a.w, b.x, b.y};
+        fma_group(g, 6, wl);
+    };
+    // the first poll reads of step i, issued ahead of its own-entry FMAs
     unsigned long long first_read[2] = {0, 0};
     auto first_poll = [&](int i) {
         const unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3 + (size_t)row * H3;
         first_read[0] = rec::load_word(slotp + pidx0);
         first_read[1] = rec::load_word(slotp + pidx1);
     };
-    auto local_fmas = [&]() {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-        float g0 = gloc[24 * wave + (lane & 15)];
-        float g1 = gloc[24 * wave + 16 + (lane & 7)];
-        rec::dpp_src_guard(g0);
-        rec::dpp_src_guard(g1);
-        dot_range1<0, 16>(acc, g0, w);
-        dot_range1<0, 8>(acc, g1, w + 16);
-    };
     // one timestep (i-th from the end): its G words are published and its
-    // own-slot FMAs done; false when the workgroup must stop
+    // own-entry FMAs done; false when the workgroup must stop
     auto step = [&](int i, float (&cur)[6], const float (&nxt)[6]) -> bool {
         // @probe:step_begin
         const int t = T - 1 - i;
@@ -907,9 +952,21 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
             gr1 = pv1 ? __uint_as_float((unsigned)wd[1]) : 0.f;
             if (!ok) s_abort = 1;
         }
-        float rows[4], rows1[4];
-        rec::rows_of(gr0, rows);
-        rec::rows_of(gr1, rows1);
+        // polled entry e of the wave to row e / 18, position e % 18 of its LDS
+        // block (one wave writes and reads the block; LDS keeps a wave's
+        // accesses in order)
+        grem[wave][lane / 18][lane % 18] = gr0;
+        if (lane < 8) grem[wave][(64 + lane) / 18][(64 + lane) % 18] = gr1;
+        __builtin_amdgcn_wave_barrier();
+        float g[20];
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const float4 v = *reinterpret_cast<const float4*>(&grem[wave][rho][4 * k]);
+            g[4 * k] = v.x;
+            g[4 * k + 1] = v.y;
+            g[4 * k + 2] = v.z;
+            g[4 * k + 3] = v.w;
+        }
         if (owner) {
             float* op = gout + ((size_t)row * T + t) * 4 * H;
             op[u] = o_dan;
@@ -919,15 +976,11 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
             if (t - 2 >= p.t_begin) load_inputs(cur, t - 2);
         }
         // @probe:polled
+        fma_group(g, 18, wm);
+        float tot[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) rec::dpp_src_guard(rows[v]);
-        rec::dpp_src_guard(rows1[0]);
-        dot_range1<0, 16>(acc, rows[0], w + 24);
-        dot_range1<0, 16>(acc, rows[1], w + 40);
-        dot_range1<0, 16>(acc, rows[2], w + 56);
-        dot_range1<0, 16>(acc, rows[3], w + 72);
-        dot_range1<0, 8>(acc, rows1[0], w + 88);
-        part[i & 1][wave][lane] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+        for (int v = 0; v < 4; ++v) tot[v] = rows_total(acc[0][v] + acc[1][v]);
+        if (rho == 0) *reinterpret_cast<float4*>(&part[i & 1][wave][4 * q]) = make_float4(tot[0], tot[1], tot[2], tot[3]);
         // @probe:computed
         __syncthreads();
         // @probe:synced
