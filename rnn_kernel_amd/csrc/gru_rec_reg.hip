@@ -745,14 +745,19 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
     if (owner) dh0[(size_t)prow * H + u] = aborted ? __builtin_nanf("") : dh;
 }
 
-// Sum of x over the four 16-lane rows, in every row: (X0 + X2) + (X1 + X3).
-__device__ __forceinline__ float rows_total(float x) {
-    const unsigned ux = __float_as_uint(x);
-    const auto a = __builtin_amdgcn_permlane32_swap(ux, ux, false, false);  // (X0 X1 X0 X1), (X2 X3 X2 X3)
-    const float sum = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const unsigned us = __float_as_uint(sum);
-    const auto b = __builtin_amdgcn_permlane16_swap(us, us, false, false);  // (S0 S0 S2 S2), (S1 S1 S3 S3)
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+// Transposed sum over the four 16-lane rows: given t[v] (v = 0..3) in every
+// row, returns in row r the sum of t[r] over the rows, (R0 + R2) + (R1 + R3).
+// v_permlane32_swap(x, y) -> (x.R0 x.R1 y.R0 y.R1), (x.R2 x.R3 y.R2 y.R3);
+// v_permlane16_swap(x, y) -> (x.R0 y.R0 x.R2 y.R2), (x.R1 y.R1 x.R3 y.R3).
+__device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
+    auto sw32 = [](float x, float y) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+        return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    };
+    const float s02 = sw32(t[0], t[2]);  // rows 0,1: t0 pairs; rows 2,3: t2 pairs
+    const float s13 = sw32(t[1], t[3]);
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(s02), __float_as_uint(s13), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
 // Backward recurrence for one batch row per workgroup at 193 <= H <= 256
@@ -767,9 +772,11 @@ __device__ __forceinline__ float rows_total(float x) {
 // over a row (ds_read_b128 from LDS, one address per row): plain v_fmac_f32
 // issues at ~1.2 ns per SIMD with two waves per SIMD on MI355X against
 // ~2.0 ns for the row-broadcast DPP form, and with four FMAs per value the
-// broadcast reads (1 KB per instruction) stay within LDS bandwidth.  Row
-// partials are summed across the wave's rows with permlane swaps, then
-// across the 8 waves in LDS.  At the end of a step the owner reduces dh,
+// broadcast reads (1 KB per instruction) stay within LDS bandwidth.  The
+// four rows' partials of a lane's four units are summed by a transposing
+// reduction (three permlane swaps leave unit 4 q + r's total in row r;
+// summing each unit in every row took eight and cost ~45 ns more per step),
+// then across the 8 waves in LDS.  At the end of a step the owner reduces dh,
 // runs the next step's pointwise math, publishes its G words and writes
 // them to LDS; after a second barrier every wave runs the own entries' FMAs
 // while the other slices' words travel.
@@ -979,8 +986,9 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         fma_group(g, 18, wm);
         float tot[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) tot[v] = rows_total(acc[0][v] + acc[1][v]);
-        if (rho == 0) *reinterpret_cast<float4*>(&part[i & 1][wave][4 * q]) = make_float4(tot[0], tot[1], tot[2], tot[3]);
+        for (int v = 0; v < 4; ++v) tot[v] = acc[0][v] + acc[1][v];
+        // row rho holds the wave's total for unit 4 q + rho
+        part[i & 1][wave][4 * q + rho] = rows_transpose_sum(tot);
         // @probe:computed
         __syncthreads();
         // @probe:synced
