@@ -121,8 +121,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
     const int B = p.B, T = p.T, H = p.H;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int g = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
+    const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
+    const int g = gc.g;
+    const int s = gc.s;
     const int u = s * 64 + lane;
     const bool uvalid = u < H;
     const int row0 = g * ROWS;
@@ -189,8 +190,8 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
     }
     if (threadIdx.x == 0) s_abort = 0;
     __shared__ int s_local;
-    // the group = the S workgroups g + k G; plain publishing stores when they share an XCD
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
+    // the group = the S workgroups of rec::group_coords; plain publishing stores when they share an XCD
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
 
     // Lane l polls k = kbeg + 64 q + l (NP words per lane); the 16-value
     // groups the row-broadcast FMAs consume are then built in registers.
@@ -355,8 +356,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     const int B = p.B, T = p.T, H = p.H;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
+    const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
+    const int row = gc.g;
+    const int s = gc.s;
     const int u = s * 64 + lane;
     const bool uvalid = u < H;
     auto kof = [&](int j, int i) { return 64 * ((s + j) & 3) + 8 * wave + i; };
@@ -417,7 +419,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     }
     if (threadIdx.x == 0) s_abort = 0;
     __shared__ int s_local;
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, row, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
 
     // Lane l < 24 polls slot 1 + l / 8, entry l % 8; other lanes, and lanes
     // of a k past H, re-read the wave's first valid remote word.
@@ -582,8 +584,9 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
     const int H3 = 3 * H;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int g = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
+    const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
+    const int g = gc.g;
+    const int s = gc.s;
     const int u = s * 64 + lane;
     const bool uvalid = u < H;
     const int row0 = g * ROWS;
@@ -628,7 +631,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_reg_kernel(
     }
     if (threadIdx.x == 0) s_abort = 0;
     __shared__ int s_local;
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
 
     // Lane l polls j = jbeg + 64 p + l (see the forward).
     constexpr int NV = NJ / 16;
@@ -794,8 +797,9 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     const int H3 = 3 * H;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int row = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
+    const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
+    const int row = gc.g;
+    const int s = gc.s;
     const int u = s * 64 + lane;  // the owner lane's unit
     const bool uvalid = u < H;
     const int rho = lane >> 4, q = lane & 15;
@@ -868,7 +872,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     }
     if (threadIdx.x == 0) s_abort = 0;
     __shared__ int s_local;
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, row, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
 
     // Wave w polls remote entries 72 w .. 72 w + 71: register 0 lane l entry
     // 72 w + l, register 1 lane l entry 72 w + 64 + l % 8.  Lanes without a
@@ -1121,12 +1125,12 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                         (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchCooperativeKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
     } else {
         void* args[] = {(void*)&a.dy, (void*)&a.dhn, (void*)&a.reserve, (void*)&a.h0, (void*)&a.y,
                         (void*)&a.w_hh, (void*)&a.gout, (void*)&a.dh0, (void*)&a.exch, (void*)&a.abort_flag,
                         (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchCooperativeKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
     }
     return 0;
 }

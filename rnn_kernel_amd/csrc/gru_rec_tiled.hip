@@ -103,8 +103,9 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
     const int wave = tid >> 6;
     const int pw = wave % PW;
     const int kc = wave / PW;
-    const int g = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
+    const GroupCoords gc = group_coords(p.G, p.S);
+    const int g = gc.g;
+    const int s = gc.s;
     const int pair = pw * 64 + lane;
     const int bl = pair / p.U;
     const int ul = pair - bl * p.U;
@@ -148,8 +149,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
     const float* hrow = hl + bl * RP;
     bool aborted = false;
     __shared__ int s_local;
-    // the group = the S workgroups g + k G; plain publishing stores when they share an XCD
-    const bool xlocal = group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
+    // the group = the S workgroups of rec::group_coords; plain publishing stores when they share an XCD
+    const bool xlocal = group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
     __syncthreads();
 
     for (int t = 0; t < T; ++t) {
@@ -241,8 +242,9 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     const int wave = tid >> 6;
     const int pw = wave % PW;
     const int kc = wave / PW;
-    const int g = blockIdx.x % p.G;
-    const int s = blockIdx.x / p.G;
+    const GroupCoords gc = group_coords(p.G, p.S);
+    const int g = gc.g;
+    const int s = gc.s;
     const int pair = pw * 64 + lane;
     const int bl = pair / p.U;
     const int ul = pair - bl * p.U;
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     bool aborted = false;
     float ddirect = 0.f;
     __shared__ int s_local;
-    const bool xlocal = group_on_one_xcd(p.xcc_words, g, p.G, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal = group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
     __syncthreads();
 
     // global step i = T-1-t over the time range (tags and slots continue
@@ -467,13 +469,13 @@ int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t st
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                         (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchCooperativeKernel(k, dim3(c.groups * c.slices), dim3(rec::NTH), args,
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(rec::NTH), args,
                                                      (unsigned)c.lds_bytes, stream));
     } else {
         void* args[] = {(void*)&a.dy, (void*)&a.dhn, (void*)&a.reserve, (void*)&a.h0, (void*)&a.y,
                         (void*)&a.w_hh, (void*)&a.gout, (void*)&a.dh0, (void*)&a.exch, (void*)&a.abort_flag,
                         (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchCooperativeKernel(k, dim3(c.groups * c.slices), dim3(rec::NTH), args,
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(rec::NTH), args,
                                                      (unsigned)c.lds_bytes, stream));
     }
     return 0;

@@ -1,8 +1,9 @@
 // Recurrence dispatcher: picks the kernel family and decomposition for a
-// shape, zeroes the exchange slots and launches one cooperative kernel.
+// shape, zeroes the exchange slots and launches one persistent kernel.
 //
 // Families (both persistent, one launch per layer and direction, the time
-// loop inside the kernel, workgroups co-resident by cooperative launch):
+// loop inside the kernel; a plain launch, the block-to-group mapping of
+// rec::group_coords guaranteeing progress without co-residency):
 //   register-resident (gru_rec_reg.hip)  hidden <= 256, W_hh slice in VGPRs;
 //   LDS-tiled         (gru_rec_tiled.hip) any hidden whose tile fits LDS.
 #include "rec_common.h"

@@ -126,6 +126,31 @@ __device__ __forceinline__ unsigned xcc_id() {
     return v & 0xfu;
 }
 
+// Placement of this workgroup in a grid of G exchange groups of S
+// workgroups (batch-row group g, slice s).  The launch needs no
+// co-residency guarantee: workgroups are dispatched to the 8 XCDs round
+// robin (block b to XCD (b + c) mod 8) and, within an XCD, in increasing
+// block order, so a mapping in which every group precedes every later group
+// in each XCD's dispatch order always makes progress (the earliest group
+// that is not fully resident has its missing members at the heads of their
+// XCDs' queues, behind groups that can finish).
+//   G a multiple of 8: the S members of group g are consecutive in the
+//     dispatch order of one XCD: blocks x + 8 (l S + k), x = g mod 8,
+//     l = g / 8, k < S, so the group also shares that XCD's L2;
+//   otherwise: consecutive block ids g S .. g S + S - 1.
+struct GroupCoords {
+    int g, s;           // group and slice of this workgroup
+    int first, stride;  // the group's blocks: first + k stride, k < S
+};
+__device__ __forceinline__ GroupCoords group_coords(int G, int S) {
+    const int b = blockIdx.x;
+    if (G % 8 == 0) {
+        const int x = b % 8, q = b / 8, l = q / S, k = q % S;
+        return {x + 8 * l, k, x + 8 * l * S, 8};
+    }
+    return {b / S, b % S, (b / S) * S, 1};
+}
+
 // Whether every member of this workgroup's exchange group (blocks first +
 // k * stride, k < count, this one included) runs on this workgroup's XCD.
 // Each workgroup publishes {xcc, tag} at words[blockIdx.x] with an

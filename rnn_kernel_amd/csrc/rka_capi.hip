@@ -38,9 +38,6 @@ int current_device_info(const DeviceInfo** out) {
         info->max_lds_per_block = (int)prop.sharedMemPerBlock;
         info->arch = prop.gcnArchName;
         info->gfx950 = info->arch.rfind("gfx950", 0) == 0;
-        int coop = 0;
-        RKA_RETURN_IF_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-        info->cooperative = coop != 0;
         g_devs[dev] = info;
     }
     *out = g_devs[dev];
@@ -48,8 +45,6 @@ int current_device_info(const DeviceInfo** out) {
         return fail(RKA_ERR_UNSUPPORTED_DEVICE,
                     "rnn_kernel_amd is built for gfx950 (MI355X); device " + std::to_string(dev) + " is " +
                         (*out)->arch);
-    if (!(*out)->cooperative)
-        return fail(RKA_ERR_UNSUPPORTED_DEVICE, "device does not support cooperative launch");
     return 0;
 }
 

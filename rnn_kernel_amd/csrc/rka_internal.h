@@ -38,7 +38,6 @@ struct DeviceInfo {
     int num_cus = 0;
     int max_lds_per_block = 0;
     bool gfx950 = false;
-    bool cooperative = false;
     std::string arch;
 };
 // Cached per device; returns 0 or an error code.

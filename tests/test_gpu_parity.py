@@ -275,12 +275,13 @@ def test_recurrence_reserve_layout_matches_oracle_cache(gpu, oracle, hip_lib):
 def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H, local):
     """Each recurrence workgroup records {XCC id, launch tag} in the workspace
     (after the two [B, 4H] exchange slots) and publishes with plain stores
-    only when its exchange group (blocks g + k G) shares one XCD.  Workgroups
-    are dispatched to the 8 XCDs round-robin (consecutive block ids on
-    consecutive XCDs, from a starting XCD that varies by launch), so the
-    groups share an XCD exactly when the group count is a multiple of 8 (the
-    bench shape among them); the others take the agent-scope path, and both
-    give the oracle's results in the layer tests."""
+    only when its exchange group shares one XCD.  Workgroups are dispatched
+    to the 8 XCDs round-robin (consecutive block ids on consecutive XCDs,
+    from a starting XCD that varies by launch).  With a group count G that is
+    a multiple of 8 (the bench shape among them) the S members of group g
+    are blocks g % 8 + 8 ((g // 8) S + k), all on one XCD; otherwise they are
+    the consecutive blocks g S + k and take the agent-scope path.  Both give
+    the oracle's results in the layer tests."""
     from rnn_kernel_amd import _lib
 
     T = 3
@@ -307,7 +308,13 @@ def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H, local):
     xcc = (words & 0xFFFFFFFF).tolist()
     assert all(t == 1 for t in tags), tags
     assert all(0 <= x < 16 for x in xcc)
-    on_one = [len({xcc[gi + k * groups] for k in range(slices)}) == 1 for gi in range(groups)]
+    def members(gi):
+        if groups % 8 == 0:
+            return [gi % 8 + 8 * ((gi // 8) * slices + k) for k in range(slices)]
+        return [gi * slices + k for k in range(slices)]
+
+    assert sorted(b for gi in range(groups) for b in members(gi)) == list(range(groups * slices))
+    on_one = [len({xcc[b] for b in members(gi)}) == 1 for gi in range(groups)]
     print(f"B={B} H={H} groups={groups} slices={slices} xcc of the first blocks {xcc[:16]} "
           f"groups on one XCD: {sum(on_one)}/{groups}", flush=True)
     assert all(on_one) == local
@@ -403,6 +410,45 @@ def test_repeat_runs_are_bitwise_identical(gpu):
                        [p.grad.clone() for p in model.parameters()])
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B,H", [(64, 256), (12, 256), (64, 96)])
+def test_recurrences_progress_beside_a_concurrent_kernel(gpu, B, H):
+    """The recurrences are launched without a co-residency guarantee: each
+    exchange group's workgroups are consecutive in the dispatch order of the
+    XCDs, so the kernel progresses when only part of the grid fits at first.
+    Here long GEMMs on a second stream hold the GPU when a layer's forward and
+    backward are enqueued; the results must equal the solo run bit for bit
+    (B=64: groups on one XCD; B=12: groups of consecutive blocks; H=96: two
+    slices)."""
+    from rnn_kernel_amd import GRU
+
+    print(f"progress beside a concurrent GEMM B={B} H={H}", flush=True)
+    torch.manual_seed(B + H)
+    model = GRU(64, H).to(gpu)
+    x = torch.randn(B, 96, 64, device=gpu)
+    big = torch.randn(6144, 6144, device=gpu)
+    side = torch.cuda.Stream(device=gpu)
+
+    def run():
+        model.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        y, hn = model(xi)
+        (y.sin().sum() + hn.sum()).backward()
+        return [y.detach().clone(), hn.detach().clone(), xi.grad.clone()] + [p.grad.clone() for p in model.parameters()]
+
+    solo = run()
+    torch.cuda.synchronize()
+    for _ in range(2):
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                big = torch.mm(big, big) * 1e-4
+        busy = run()
+        torch.cuda.synchronize()
+        for a, b in zip(solo, busy):
+            assert torch.isfinite(b).all()
+            assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("kind,units,param", [(1, 1, 0), (1, 4, 0), (1, 16, 2), (1, 64, 0), (2, 0, 2), (2, 0, 4)])
