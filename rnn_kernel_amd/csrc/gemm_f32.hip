@@ -374,46 +374,59 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     }
 }
 
-// out[o*ldc + n] = sum_z partial[z][(o+rot)%m][n] (z in order); colsum
-// likewise.  With vec, a thread sums one float4 of a row.
+// out[o*ldc + n] = sum_z partial[z][(o+rot)%m][n]; colsum likewise.  With
+// vec, a team of kTeam threads (consecutive lanes) sums one float4 of a row:
+// member r takes slices r, r + kTeam, ... in order, then the team's sums are
+// added as a fixed tree, so the order is the same on every run.
+constexpr int kTeam = 8;
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int ksplit,
                                                             int m, int n, int rot, float* __restrict__ c,
                                                             int ldc, float* __restrict__ colsum, int vec) {
     const size_t per_row = vec ? (size_t)(n / 4) : (size_t)n;
     const size_t items = (size_t)m * per_row;
     const size_t total = items + (colsum ? m : 0);
-    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (size_t)gridDim.x * blockDim.x) {
+    const int member = threadIdx.x % kTeam;
+    const size_t teams = (size_t)gridDim.x * (blockDim.x / kTeam);
+    for (size_t idx = (size_t)blockIdx.x * (blockDim.x / kTeam) + threadIdx.x / kTeam; idx < total; idx += teams) {
         if (idx < items) {
             const int o = (int)(idx / per_row);
             const int src = rot ? (o + rot) % m : o;
             if (vec) {
                 const int col = 4 * (int)(idx % per_row);
                 const float* pp = partial + (size_t)src * n + col;
-                float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-                for (int z = 0; z < ksplit; ++z) {
+                float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int z = member; z < ksplit; z += kTeam) {
                     const float4 v = *reinterpret_cast<const float4*>(pp + (size_t)z * m * n);
-                    s.x += v.x;
-                    s.y += v.y;
-                    s.z += v.z;
-                    s.w += v.w;
+                    s4.x += v.x;
+                    s4.y += v.y;
+                    s4.z += v.z;
+                    s4.w += v.w;
                 }
-                *reinterpret_cast<float4*>(c + (size_t)o * ldc + col) = s;
+#pragma unroll
+                for (int off = 1; off < kTeam; off <<= 1) {
+                    s4.x += __shfl_xor(s4.x, off, kTeam);
+                    s4.y += __shfl_xor(s4.y, off, kTeam);
+                    s4.z += __shfl_xor(s4.z, off, kTeam);
+                    s4.w += __shfl_xor(s4.w, off, kTeam);
+                }
+                if (member == 0) *reinterpret_cast<float4*>(c + (size_t)o * ldc + col) = s4;
             } else {
                 const int col = (int)(idx % per_row);
-                float s = 0.f;
-#pragma unroll 8
-                for (int z = 0; z < ksplit; ++z) s += partial[((size_t)z * m + src) * n + col];
-                c[(size_t)o * ldc + col] = s;
+                float sum = 0.f;
+                for (int z = member; z < ksplit; z += kTeam) sum += partial[((size_t)z * m + src) * n + col];
+#pragma unroll
+                for (int off = 1; off < kTeam; off <<= 1) sum += __shfl_xor(sum, off, kTeam);
+                if (member == 0) c[(size_t)o * ldc + col] = sum;
             }
         } else {
             const int o = (int)(idx - items);
             const int src = rot ? (o + rot) % m : o;
             const float* cpart = partial + (size_t)ksplit * m * n;
-            float s = 0.f;
-            for (int z = 0; z < ksplit; ++z) s += cpart[(size_t)z * m + src];
-            colsum[o] = s;
+            float sum = 0.f;
+            for (int z = member; z < ksplit; z += kTeam) sum += cpart[(size_t)z * m + src];
+#pragma unroll
+            for (int off = 1; off < kTeam; off <<= 1) sum += __shfl_xor(sum, off, kTeam);
+            if (member == 0) colsum[o] = sum;
         }
     }
 }
@@ -536,7 +549,7 @@ int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot,
                   float* colsum, hipStream_t stream) {
     const int vec = (n % 4 == 0 && ldc % 4 == 0 && aligned16(partial) && aligned16(c)) ? 1 : 0;
     const size_t total = (size_t)m * (vec ? n / 4 : n) + (colsum ? m : 0);
-    const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+    const int blocks = (int)std::min<size_t>((total * kTeam + 255) / 256, 8192);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, ksplit_total, m, n,
                        rot, c, ldc, colsum, vec);
     RKA_RETURN_IF_HIP(hipGetLastError());
