@@ -6,9 +6,10 @@
 //   weight gradients  dW  = G^T [X | Hprev]        (A k-major,  B k-major)
 // C[m,n] = sum_k A(m,k) B(n,k).  A workgroup of 4 wavefronts computes a
 // 128x128 tile; each wavefront owns a 64x64 quadrant as 4x4 MFMA 16x16
-// blocks.  Operand tiles of 16 (direct) or 32 (split-K) k are staged through
-// double-buffered LDS (the next tile is loaded into registers while the
-// current one is consumed; one barrier per tile).  The LDS forms are chosen
+// blocks.  Operand tiles of 16 k are staged through double-buffered LDS
+// (the next tile is loaded into registers while the current one is
+// consumed; one barrier per tile; three workgroups per CU).  The LDS forms
+// are chosen
 // so that every MFMA operand read is one conflict-free ds_read_b128 feeding
 // four MFMAs: A keeps the form of its global layout (row-major tiles give a
 // lane four k of one row, k-major tiles four rows at one k) and B is kept
@@ -64,7 +65,7 @@ __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, i
 // KMAJOR == 0: thread -> (row tid/KQ + (NT/KQ) i, k 4*(tid%KQ) .. +3), KQ = BK/4
 // KMAJOR == 1: thread -> (k tid/32 + (NT/32) i, row 4*(tid%32) .. +3)
 constexpr int kDirectBK = 16;
-constexpr int kSplitBK = 32;
+constexpr int kSplitBK = 16;
 static_assert(BM == 128 && BN == 128 && NT == 256, "tile staging layout");
 
 template <int KMAJOR, bool SHIFT, bool SEG, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>

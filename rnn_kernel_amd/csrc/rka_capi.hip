@@ -106,7 +106,7 @@ BwdLayout bwd_layout(int B, int T, int I, int H) {
     BwdLayout l{};
     l.nc = backward_chunks(T);
     const int Kc = B * chunk_len(T, l.nc, 0);
-    const int wgs = l.nc > 1 ? 0 : 2;
+    const int wgs = l.nc > 1 ? 0 : 3;  // resident split-K workgroups per CU
     l.ks_hh = choose_ksplit(3 * H, H, Kc, 256, wgs);
     l.ks_ih = choose_ksplit(3 * H, I, Kc, 256, wgs);
     l.g = 0;

@@ -68,15 +68,20 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
 
 def test_backward_chunk_policy_without_gpu(hip_lib):
     """Automatic: one time chunk; an override is clamped to seq_len; the
-    workspace grows by the dh carry buffers."""
+    chunked layout holds the G buffer, the exchange words, per-chunk split-K
+    partials and the two dh carry buffers."""
     from rnn_kernel_amd import _lib
 
+    B, T, I, H = 64, 100, 256, 256
     try:
         assert _lib.backward_chunks(512) == 1 and _lib.backward_chunks(127) == 1
-        one = hip_lib.rka_gru_backward_workspace_bytes(64, 100, 256, 256)
+        one = hip_lib.rka_gru_backward_workspace_bytes(B, T, I, H)
         _lib.set_backward_chunks(3)
         assert _lib.backward_chunks(2) == 2 and _lib.backward_chunks(512) == 3
-        assert hip_lib.rka_gru_backward_workspace_bytes(64, 100, 256, 256) > one
+        chunked = hip_lib.rka_gru_backward_workspace_bytes(B, T, I, H)
+        g_bytes, carry_bytes = B * T * 4 * H * 4, 2 * B * H * 4
+        assert chunked != one
+        assert chunked > g_bytes + hip_lib.rka_gru_recurrence_workspace_bytes(B, H) + carry_bytes
     finally:
         _lib.set_backward_chunks(0)
 
