@@ -212,13 +212,13 @@ __device__ __forceinline__ void split_coords(const GemmArgs& p, int& bx, int& by
 //   A in k form:   block a, MFMA row i = tile row 4 i + a;
 //   B (k form):    block b, MFMA column c = tile column 4 c + b,
 // so a lane's four B blocks are four adjacent output columns (float4 stores).
-template <int ALF, int BK>
+template <int ALF, int BK, int KS = LDSP>
 __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int lane, int wm, int wn, int tid,
                                          bool colsum, float& cs, floatx4 (&acc)[4][4]) {
     if (colsum && tid < BM) {
         // column sums of A (bias gradients of split-K products; A in k form)
 #pragma unroll
-        for (int kk = 0; kk < BK; ++kk) cs += as[kk * LDSP + tid];
+        for (int kk = 0; kk < BK; ++kk) cs += as[kk * KS + tid];
     }
     const int i = lane & 15, g = lane >> 4;
     constexpr int NS = BK / 16;
@@ -232,8 +232,8 @@ __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int l
             if constexpr (ALF == 0)
                 fa[q][x] = *reinterpret_cast<const float4*>(as + (wm * 64 + 16 * x + i) * (BK + 4) + 16 * q + 4 * g);
             else
-                fa[q][x] = *reinterpret_cast<const float4*>(as + (16 * q + 4 * g + x) * LDSP + wm * 64 + 4 * i);
-            fb[q][x] = *reinterpret_cast<const float4*>(bs + (16 * q + 4 * g + x) * LDSP + wn * 64 + 4 * i);
+                fa[q][x] = *reinterpret_cast<const float4*>(as + (16 * q + 4 * g + x) * KS + wm * 64 + 4 * i);
+            fb[q][x] = *reinterpret_cast<const float4*>(bs + (16 * q + 4 * g + x) * KS + wn * 64 + 4 * i);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -293,6 +293,69 @@ __device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int 
     }
 }
 
+// Both operands k-major, interior tile, whole k-tiles: the operand tiles go
+// from global memory straight to LDS (global_load_lds_dwordx4, 16 bytes per
+// lane, a wave's 64 lanes filling 1 KB = two k rows of a [16][128] tile)
+// through a ring of three stages, so tile kb+2 is in flight while tile kb
+// is consumed, without staging registers.  One barrier per k-tile: it
+// follows a wait for this wave's part of stage kb (the next stage's four
+// loads may stay in flight) and precedes the loads into the stage consumed
+// two tiles ago.  The barrier is the bare s_barrier (no fence): the wait
+// covers this wave's loads, and every wave waits before it.
+// The wave's 64 lanes each copy 16 bytes from src to LDS address
+// M0 + 16 * lane, M0 = the wave's destination (wave-uniform).  Written as
+// inline assembly so the compiler does not place a wait for every
+// outstanding LDS load before each LDS read (it cannot tell the stages
+// apart); the loop below waits on the vector-memory counter itself.  The
+// s_nop covers the one wait state an M0 write needs before an LDS-DMA load.
+// (M0 is declared clobbered; no other code of these kernels uses it, which
+// the compiler's reserved-register warning cannot know.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const float* src, float* lds_dst) {
+    const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+constexpr int kDmaStages = 3;
+constexpr int kDmaTile = 16 * BM;  // floats per operand tile
+template <bool BSHIFT, bool SEG>
+__device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, int kbeg, int nkb, int tid, int lane,
+                                             int wm, int wn, bool colsum, float& cs, float* smem,
+                                             floatx4 (&acc)[4][4]) {
+    const int wave = tid >> 6;
+    auto a_stage = [&](int st) { return smem + st * 2 * kDmaTile; };
+    auto b_stage = [&](int st) { return smem + st * 2 * kDmaTile + kDmaTile; };
+    auto issue = [&](int kb, int st) {
+        const int k0 = kbeg + kb * 16;
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const int kr = 4 * wave + 2 * d;  // first k row of this wave's 1 KB block
+            const int kk = k0 + kr + (lane >> 5), col = 4 * (lane & 31);
+            lds_dma16(elem_ptr<1, false, SEG>(p.a, m0 + col, kk), a_stage(st) + kr * BM);
+            lds_dma16(elem_ptr<1, BSHIFT, SEG>(p.b, n0 + col, kk), b_stage(st) + kr * BM);
+        }
+    };
+    issue(0, 0);
+    if (nkb > 1) issue(1, 1);
+    for (int kb = 0; kb < nkb; ++kb) {
+        // this wave's four loads of stage kb are done once at most the next
+        // stage's four are outstanding (gfx9 s_waitcnt: vmcnt in bits 3:0,
+        // expcnt and lgkmcnt left at their maxima)
+        if (kb + 1 < nkb)
+            __builtin_amdgcn_s_waitcnt(0x0F74);
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kb + 2 < nkb) issue(kb + 2, (kb + 2) % kDmaStages);
+        mma_tile<1, 16, BM>(a_stage(kb % kDmaStages), b_stage(kb % kDmaStages), lane, wm, wn, tid, colsum, cs, acc);
+    }
+}
+
 // The same loop with the operand tiles loaded two k-tiles ahead into
 // alternating register sets: the loads of tile kb+2 are issued before the
 // MFMAs of tile kb and stored to LDS at the end of iteration kb+1, so a
@@ -338,7 +401,10 @@ template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? k
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     constexpr int AF = lds_tile_floats<AK, BK>();
     constexpr int BF = lds_tile_floats<1, BK>();
-    __shared__ __attribute__((aligned(16))) float smem[2 * AF + 2 * BF];
+    constexpr bool kDma = AK == 1 && BKM == 1 && BK == 16;
+    constexpr int kSmem = kDma && kDmaStages * 2 * kDmaTile > 2 * AF + 2 * BF ? kDmaStages * 2 * kDmaTile
+                                                                              : 2 * AF + 2 * BF;
+    __shared__ __attribute__((aligned(16))) float smem[kSmem];
     float* As0 = smem;
     float* As1 = smem + AF;
     float* Bs0 = smem + 2 * AF;
@@ -367,6 +433,9 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     if constexpr (!SPLIT && AK == 0 && BKM == 1)
         mainloop_deep<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1,
                                                 Bs0, Bs1, acc);
+    else if (kDma && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 &&
+             (kend - kbeg) % BK == 0)
+        mainloop_dma<BSHIFT, SEG>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, smem, acc);
     else
         mainloop<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
                                            Bs1, acc);
