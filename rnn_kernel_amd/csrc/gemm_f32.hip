@@ -6,18 +6,17 @@
 //   weight gradients  dW  = G^T [X | Hprev]        (A k-major,  B k-major)
 // C[m,n] = sum_k A(m,k) B(n,k).  A workgroup of 4 wavefronts computes a
 // 128x128 tile; each wavefront owns a 64x64 quadrant as 4x4 MFMA 16x16
-// blocks.  Operand tiles of 16 k are staged through double-buffered LDS
-// (the next tile is loaded into registers while the current one is
-// consumed; one barrier per tile; three workgroups per CU).  The LDS forms
-// are chosen
-// so that every MFMA operand read is one conflict-free ds_read_b128 feeding
-// four MFMAs: A keeps the form of its global layout (row-major tiles give a
-// lane four k of one row, k-major tiles four rows at one k) and B is kept
-// k-major, which also makes a lane's four B blocks four adjacent output
-// columns, stored as one float4.  Measured at c2 against the previous
-// v_mfma_f32_32x32x2_f32 kernel (b32 operand reads, scalar stores): input
-// projection 128 vs 141 us, dx 126 vs 133 us, dW 157/148 vs 161/154 us.
-// Each operand layout is a template instance, so no product carries
+// blocks; three workgroups per CU.  Interior tiles load their 16-deep
+// operand tiles straight from global memory into a three-stage LDS ring
+// (global_load_lds_dwordx4); edge tiles and operands that are not 16-byte
+// aligned stage them through registers into double-buffered LDS.  The LDS
+// forms are chosen so that every MFMA operand read is one conflict-free
+// ds_read_b128 feeding four MFMAs: a k-major tile is kept [k][row] (a lane
+// reads four rows at one k), a row-major one [row][k] (four k of one row;
+// swizzled in the ring, padded in the register path), and a lane's four B
+// blocks are four adjacent output columns, stored as one float4.  At c2:
+// input projection 124 us, dx 111 us, dW 135/130 us (the register-staged
+// loop alone: 128, 121, 143/133 us).  Each operand layout is a template instance, so no product carries
 // another's address arithmetic.  The weight gradients (K = B*T rows) use
 // split-K with a fixed-order reduction, so results are deterministic run to
 // run.
@@ -212,15 +211,25 @@ __device__ __forceinline__ void split_coords(const GemmArgs& p, int& bx, int& by
 //   A in k form:   block a, MFMA row i = tile row 4 i + a;
 //   B (k form):    block b, MFMA column c = tile column 4 c + b,
 // so a lane's four B blocks are four adjacent output columns (float4 stores).
-template <int ALF, int BK, int KS = LDSP>
+// LDS forms: 0 = row form [row][BK+4]; 1 = k form [k][KS]; 2 = the
+// swizzled row form of the direct-to-LDS loads (swz_slot below, BK = 16).
+// A in form 2 has the block rows of the row form; B in form 2 the block
+// columns of the k form.
+template <int ALF, int BK, int KS = LDSP, int BLF = 1>
 __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int lane, int wm, int wn, int tid,
                                          bool colsum, float& cs, floatx4 (&acc)[4][4]) {
-    if (colsum && tid < BM) {
-        // column sums of A (bias gradients of split-K products; A in k form)
+    static_assert((ALF != 2 && BLF != 2) || BK == 16, "swizzled row form holds 16-deep tiles");
+    if constexpr (ALF == 1) {
+        if (colsum && tid < BM) {
+            // column sums of A (bias gradients of split-K products; A in k form)
 #pragma unroll
-        for (int kk = 0; kk < BK; ++kk) cs += as[kk * KS + tid];
+            for (int kk = 0; kk < BK; ++kk) cs += as[kk * KS + tid];
+        }
     }
     const int i = lane & 15, g = lane >> 4;
+    // form 2: a lane's chunk offset within its 16-row group (rows 16 a + i of A,
+    // rotated columns of B), the k quad g swizzled by bits 2..3 of i
+    const int sw = 16 * i + 4 * (g ^ ((i >> 2) & 3));
     constexpr int NS = BK / 16;
     // every operand fragment of the tile first (distinct registers), so the
     // MFMAs of a slab do not wait on LDS reads issued behind earlier MFMAs
@@ -231,9 +240,14 @@ __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int l
         for (int x = 0; x < 4; ++x) {
             if constexpr (ALF == 0)
                 fa[q][x] = *reinterpret_cast<const float4*>(as + (wm * 64 + 16 * x + i) * (BK + 4) + 16 * q + 4 * g);
+            else if constexpr (ALF == 2)
+                fa[q][x] = *reinterpret_cast<const float4*>(as + 16 * (wm * 64 + 16 * x) + sw);
             else
                 fa[q][x] = *reinterpret_cast<const float4*>(as + (16 * q + 4 * g + x) * KS + wm * 64 + 4 * i);
-            fb[q][x] = *reinterpret_cast<const float4*>(bs + (16 * q + 4 * g + x) * KS + wn * 64 + 4 * i);
+            if constexpr (BLF == 2)
+                fb[q][x] = *reinterpret_cast<const float4*>(bs + 16 * (wn * 64 + 16 * x) + sw);
+            else
+                fb[q][x] = *reinterpret_cast<const float4*>(bs + (16 * q + 4 * g + x) * KS + wn * 64 + 4 * i);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -243,22 +257,23 @@ __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int l
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
             for (int a = 0; a < 4; ++a) {
-                // row form: fa[q][block a] holds steps 0..3; k form: fa[q][step j] holds blocks 0..3
-                const float av = ALF == 0 ? fa[q][a][j] : fa[q][j][a];
+                // row forms: fa[q][block a] holds steps 0..3; k form: fa[q][step j] holds blocks 0..3
+                const float av = ALF != 1 ? fa[q][a][j] : fa[q][j][a];
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, fb[q][j][b], acc[a][b], 0, 0, 0);
+                for (int b = 0; b < 4; ++b) {
+                    const float bv = BLF == 2 ? fb[q][b][j] : fb[q][j][b];
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[a][b], 0, 0, 0);
+                }
             }
         }
     }
 }
 
-// The k loop: the next k-tile is loaded into registers while the MFMAs of
-// the current one run, then stored to the other LDS buffer; one barrier per
-// k-tile.  Interior tiles of vector-capable operands load float4 without
-// bounds checks; edge tiles check per element.  (A two-deep register
-// prefetch measured slower at c2: its registers cost a resident workgroup
-// per CU.)
+// The register-staged k loop (edge tiles, unaligned operands): the next
+// k-tile is loaded into registers while the MFMAs of the current one run,
+// then stored to the other LDS buffer; one barrier per k-tile.  Interior
+// tiles of vector-capable operands load float4 without bounds checks; edge
+// tiles check per element.
 template <int AK, int BKM, bool BSHIFT, bool SEG, int BK>
 __device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int nkb,
                                                  int tid, int lane, int wm, int wn, bool colsum, float& cs,
@@ -293,15 +308,16 @@ __device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int 
     }
 }
 
-// Both operands k-major, interior tile, whole k-tiles: the operand tiles go
-// from global memory straight to LDS (global_load_lds_dwordx4, 16 bytes per
-// lane, a wave's 64 lanes filling 1 KB = two k rows of a [16][128] tile)
-// through a ring of three stages, so tile kb+2 is in flight while tile kb
-// is consumed, without staging registers.  One barrier per k-tile: it
-// follows a wait for this wave's part of stage kb (the next stage's four
-// loads may stay in flight) and precedes the loads into the stage consumed
-// two tiles ago.  The barrier is the bare s_barrier (no fence): the wait
-// covers this wave's loads, and every wave waits before it.
+// Interior tiles of vector-capable operands, whole k-tiles: the operand
+// tiles go from global memory straight to LDS (global_load_lds_dwordx4, 16
+// bytes per lane, a wave's 64 lanes filling 1 KB of a 8 KB tile) through a
+// ring of three stages, so tile kb+2 is in flight while tile kb is
+// consumed, without staging registers.  One barrier per k-tile: it follows
+// a wait for this wave's part of stage kb (the next stage's four loads may
+// stay in flight) and precedes the loads into the stage consumed two tiles
+// ago.  The barrier is the bare s_barrier (no fence): the wait covers this
+// wave's loads, and every wave waits before it.
+//
 // The wave's 64 lanes each copy 16 bytes from src to LDS address
 // M0 + 16 * lane, M0 = the wave's destination (wave-uniform).  Written as
 // inline assembly so the compiler does not place a wait for every
@@ -321,7 +337,30 @@ __device__ __forceinline__ void lds_dma16(const float* src, float* lds_dst) {
 
 constexpr int kDmaStages = 3;
 constexpr int kDmaTile = 16 * BM;  // floats per operand tile
-template <bool BSHIFT, bool SEG>
+
+// Source of 16-byte chunk s (0..511) of a stage's operand tile, rows r0..,
+// k k0..k0+15.  A load writes chunk s where it lands, so the LDS form is
+// chosen by which global chunk each lane fetches:
+//   k-major operand: k form [16][128] unpadded, chunk s = k row s/32,
+//     rows 4 (s%32) .. +3;
+//   row-major operand: swizzled row form, chunk s = tile row t = s/4 (for B
+//     the rotated column: t = 64 (n/64) + 16 (n%4) + (n%64)/4), k quad
+//     (s%4) ^ ((t/4)%4).  The 16 lanes of one ds_read_b128 (one k quad g,
+//     rows 16a + i of A or columns 4i + b of B) then fall on 16 distinct
+//     4-bank groups.
+template <int KMAJOR, bool SHIFT, bool SEG, bool ROT>
+__device__ __forceinline__ const float* dma_src(const GemmOperand& op, int r0, int k0, int s) {
+    if constexpr (KMAJOR == 1) {
+        return elem_ptr<1, SHIFT, SEG>(op, r0 + 4 * (s & 31), k0 + (s >> 5));
+    } else {
+        const int t = s >> 2;
+        const int kq = (s & 3) ^ ((t >> 2) & 3);
+        const int row = ROT ? (t & ~63) | ((t & 15) << 2) | ((t >> 4) & 3) : t;
+        return elem_ptr<0, false, SEG>(op, r0 + row, k0 + 4 * kq);
+    }
+}
+
+template <int AK, int BKM, bool BSHIFT, bool SEG>
 __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, int kbeg, int nkb, int tid, int lane,
                                              int wm, int wn, bool colsum, float& cs, float* smem,
                                              floatx4 (&acc)[4][4]) {
@@ -332,10 +371,9 @@ __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, 
         const int k0 = kbeg + kb * 16;
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
-            const int kr = 4 * wave + 2 * d;  // first k row of this wave's 1 KB block
-            const int kk = k0 + kr + (lane >> 5), col = 4 * (lane & 31);
-            lds_dma16(elem_ptr<1, false, SEG>(p.a, m0 + col, kk), a_stage(st) + kr * BM);
-            lds_dma16(elem_ptr<1, BSHIFT, SEG>(p.b, n0 + col, kk), b_stage(st) + kr * BM);
+            const int s0 = 64 * (2 * wave + d);  // first chunk of this wave's 1 KB block
+            lds_dma16(dma_src<AK, false, SEG, false>(p.a, m0, k0, s0 + lane), a_stage(st) + 4 * s0);
+            lds_dma16(dma_src<BKM, BSHIFT, SEG, true>(p.b, n0, k0, s0 + lane), b_stage(st) + 4 * s0);
         }
     };
     issue(0, 0);
@@ -352,48 +390,8 @@ __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, 
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (kb + 2 < nkb) issue(kb + 2, (kb + 2) % kDmaStages);
-        mma_tile<1, 16, BM>(a_stage(kb % kDmaStages), b_stage(kb % kDmaStages), lane, wm, wn, tid, colsum, cs, acc);
-    }
-}
-
-// The same loop with the operand tiles loaded two k-tiles ahead into
-// alternating register sets: the loads of tile kb+2 are issued before the
-// MFMAs of tile kb and stored to LDS at the end of iteration kb+1, so a
-// load has two MFMA bursts to arrive.  The extra registers cost a resident
-// workgroup per CU, so only the input gradient uses it (512 tiles at c2,
-// two per CU in any case): dx stage 122.5 vs 126.8 us at c2.
-template <int AK, int BKM, bool BSHIFT, bool SEG, int BK>
-__device__ __forceinline__ void mainloop_deep(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int nkb,
-                                              int tid, int lane, int wm, int wn, bool colsum, float& cs,
-                                              float* As0, float* As1, float* Bs0, float* Bs1,
-                                              floatx4 (&acc)[4][4]) {
-    constexpr int NV4 = BM * BK / (4 * NT);
-    const bool av = p.a_vec != 0, bv = p.b_vec != 0;
-    float4 ra0[NV4], rb0[NV4], ra1[NV4], rb1[NV4];
-    auto load = [&](int kb, float4 (&ra)[NV4], float4 (&rb)[NV4]) {
-        load_tile<AK, false, SEG, BK>(p.a, av, p.m, kend, m0, kbeg + kb * BK, tid, ra);
-        load_tile<BKM, BSHIFT, SEG, BK>(p.b, bv, p.n, kend, n0, kbeg + kb * BK, tid, rb);
-    };
-    auto step = [&](int kb, float* as, float* bs, float* as_n, float* bs_n, float4 (&fa)[NV4], float4 (&fb)[NV4],
-                    float4 (&na)[NV4], float4 (&nb)[NV4]) {
-        if (kb + 2 < nkb) load(kb + 2, fa, fb);  // this set's tile kb is in LDS already
-        mma_tile<AK, BK>(as, bs, lane, wm, wn, tid, colsum, cs, acc);
-        if (kb + 1 < nkb) {
-            store_tile<AK, AK, BK>(as_n, tid, na);
-            store_tile<BKM, 1, BK>(bs_n, tid, nb);
-        }
-        __syncthreads();
-    };
-    if (nkb > 0) {
-        load(0, ra0, rb0);
-        if (nkb > 1) load(1, ra1, rb1);
-        store_tile<AK, AK, BK>(As0, tid, ra0);
-        store_tile<BKM, 1, BK>(Bs0, tid, rb0);
-    }
-    __syncthreads();
-    for (int kb = 0; kb < nkb; kb += 2) {
-        step(kb, As0, Bs0, As1, Bs1, ra0, rb0, ra1, rb1);
-        if (kb + 1 < nkb) step(kb + 1, As1, Bs1, As0, Bs0, ra1, rb1, ra0, rb0);
+        mma_tile<AK == 1 ? 1 : 2, 16, BM, BKM == 1 ? 1 : 2>(a_stage(kb % kDmaStages), b_stage(kb % kDmaStages), lane,
+                                                           wm, wn, tid, colsum, cs, acc);
     }
 }
 
@@ -401,7 +399,7 @@ template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? k
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     constexpr int AF = lds_tile_floats<AK, BK>();
     constexpr int BF = lds_tile_floats<1, BK>();
-    constexpr bool kDma = AK == 1 && BKM == 1 && BK == 16;
+    constexpr bool kDma = BK == 16;
     constexpr int kSmem = kDma && kDmaStages * 2 * kDmaTile > 2 * AF + 2 * BF ? kDmaStages * 2 * kDmaTile
                                                                               : 2 * AF + 2 * BF;
     __shared__ __attribute__((aligned(16))) float smem[kSmem];
@@ -430,12 +428,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
         for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
     float cs = 0.f;
 
-    if constexpr (!SPLIT && AK == 0 && BKM == 1)
-        mainloop_deep<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1,
-                                                Bs0, Bs1, acc);
-    else if (kDma && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 &&
-             (kend - kbeg) % BK == 0)
-        mainloop_dma<BSHIFT, SEG>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, smem, acc);
+    if (kDma && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 && (kend - kbeg) % BK == 0)
+        mainloop_dma<AK, BKM, BSHIFT, SEG>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, smem, acc);
     else
         mainloop<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
                                            Bs1, acc);
