@@ -47,8 +47,8 @@ def stage_flops(B, T, I, H):
         "input_gemm": 2.0 * B * T * 3 * H * I,
         "forward_recurrence": 2.0 * B * T * 3 * H * H,
         "backward_recurrence": 2.0 * B * T * 3 * H * H,
-        "dw_hh_gemm": 2.0 * B * T * 3 * H * H,
-        "dw_ih_gemm": 2.0 * B * T * 3 * H * I,
+        "dw_gemm": 2.0 * B * T * 3 * H * (H + I),
+        "dw_reduce": 0.0,
         "dx_gemm": 2.0 * B * T * 3 * H * I,
     }
 

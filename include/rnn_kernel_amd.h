@@ -183,7 +183,8 @@ int rka_eval_gate_functions(const float* x, float* sigmoid_out, float* tanh_out,
  * its stream; rka_profile_read() waits for the recorded events, returns the
  * summed milliseconds and launch counts per stage and clears the records.
  * Stage ids: 0 input GEMM, 1 forward recurrence, 2 backward recurrence,
- * 3 dW_hh GEMM (+reduction), 4 dW_ih GEMM (+reduction), 5 dx GEMM.
+ * 3 dW_hh and dW_ih split-K products (one launch unless the backward runs
+ * in time chunks), 4 their split-K reductions into dW and db, 5 dx GEMM.
  */
 #define RKA_NUM_STAGES 6
 int rka_profile_enable(int on);

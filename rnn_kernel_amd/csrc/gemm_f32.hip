@@ -187,8 +187,7 @@ struct GemmArgs {
 // of 8, the tiles of one k-chunk are given consecutive ids on one XCD, so
 // the chunk's operand rows are fetched into that XCD's L2 once and re-read
 // from there by the other tiles.
-__device__ __forceinline__ void split_coords(const GemmArgs& p, int& bx, int& by, int& bz) {
-    const int id = blockIdx.x;
+__device__ __forceinline__ void split_coords(const GemmArgs& p, int id, int& bx, int& by, int& bz) {
     int tile;
     if (p.ksplit % 8 == 0) {
         const int xcd = id % 8, slot = id / 8;
@@ -395,14 +394,21 @@ __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, 
     }
 }
 
-template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
+// LDS floats of one workgroup: the three-stage ring or the two register-path
+// buffers, whichever is larger.
+template <int AK, int BK>
+constexpr int gemm_smem_floats() {
+    constexpr int AF = lds_tile_floats<AK, BK>();
+    constexpr int BF = lds_tile_floats<1, BK>();
+    return BK == 16 && kDmaStages * 2 * kDmaTile > 2 * AF + 2 * BF ? kDmaStages * 2 * kDmaTile : 2 * AF + 2 * BF;
+}
+
+// One output tile (bx, by) of k-chunk bz.
+template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int bz, float* smem) {
     constexpr int AF = lds_tile_floats<AK, BK>();
     constexpr int BF = lds_tile_floats<1, BK>();
     constexpr bool kDma = BK == 16;
-    constexpr int kSmem = kDma && kDmaStages * 2 * kDmaTile > 2 * AF + 2 * BF ? kDmaStages * 2 * kDmaTile
-                                                                              : 2 * AF + 2 * BF;
-    __shared__ __attribute__((aligned(16))) float smem[kSmem];
     float* As0 = smem;
     float* As1 = smem + AF;
     float* Bs0 = smem + 2 * AF;
@@ -412,8 +418,6 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    int bx = blockIdx.x, by = blockIdx.y, bz = 0;
-    if (SPLIT) split_coords(p, bx, by, bz);
     const int m0 = bx * BM;
     const int n0 = by * BN;
     const int kbeg = bz * p.kchunk;
@@ -480,6 +484,33 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     if (colsum && tid < BM && m0 + tid < p.m) {
         float* cpart = p.partial + (size_t)p.ksplit_total * p.m * p.n;
         cpart[(size_t)(p.z_off + bz) * p.m + m0 + tid] = cs;
+    }
+}
+
+template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
+    __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<AK, BK>()];
+    int bx = blockIdx.x, by = blockIdx.y, bz = 0;
+    if (SPLIT) split_coords(p, blockIdx.x, bx, by, bz);
+    gemm_tile<AK, BKM, BSHIFT, SPLIT, SEG, BK>(p, bx, by, bz, smem);
+}
+
+// Two split-K products of k-major operands in one launch: workgroups
+// [0, tiles0 * ksplit0) take the first, the rest the second (the weight
+// gradients dW_hh, whose B operand is row-remapped, and dW_ih).  One launch
+// of both at half the slices each keeps three workgroups per CU with half
+// the partial sums and one ramp-up and tail instead of two.
+template <bool SHIFT0, bool SEG>
+__global__ __launch_bounds__(NT) void gemm_f32_pair_kernel(GemmArgs p0, GemmArgs p1) {
+    __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<1, kSplitBK>()];
+    const int blocks0 = p0.tiles * p0.ksplit;
+    int bx, by, bz;
+    if ((int)blockIdx.x < blocks0) {
+        split_coords(p0, blockIdx.x, bx, by, bz);
+        gemm_tile<1, 1, SHIFT0, true, SEG, kSplitBK>(p0, bx, by, bz, smem);
+    } else {
+        split_coords(p1, blockIdx.x - blocks0, bx, by, bz);
+        gemm_tile<1, 1, false, true, SEG, kSplitBK>(p1, bx, by, bz, smem);
     }
 }
 
@@ -579,7 +610,7 @@ int launch_gemm_t(const GemmArgs& args, dim3 grid, hipStream_t stream) {
 }
 
 template <bool SPLIT>
-int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream) {
+void finish_args(GemmArgs& args, int ksplit, bool av, bool bv) {
     const int tm = (args.m + BM - 1) / BM, tn = (args.n + BN - 1) / BN;
     args.tiles_m = tm;
     args.tiles = tm * tn;
@@ -590,6 +621,12 @@ int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream)
         args.z_off = 0;
         args.ksplit_total = 1;
     }
+}
+
+template <bool SPLIT>
+int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream) {
+    finish_args<SPLIT>(args, ksplit, av, bv);
+    const int tm = args.tiles_m, tn = args.tiles / args.tiles_m;
     const dim3 grid = SPLIT ? dim3(tm * tn * ksplit) : dim3(tm, tn);
     const bool seg = args.a.seg.len || args.b.seg.len || args.c_seg.len;
     return seg ? launch_gemm_t<SPLIT, true>(args, grid, stream) : launch_gemm_t<SPLIT, false>(args, grid, stream);
@@ -633,12 +670,15 @@ int choose_ksplit(int m, int n, int k, int num_cus, int wgs_per_cu) {
     return ks;
 }
 
-int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum,
-                         float* partial, int ksplit, int z_off, int ksplit_total, hipStream_t stream) {
+namespace {
+int split_args(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum, float* partial,
+               int ksplit, int z_off, int ksplit_total, GemmArgs* out) {
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
     if (ksplit < 1 || z_off < 0 || z_off + ksplit > ksplit_total)
         return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: bad split slices");
-    GemmArgs args{};
+    if (!a.kmajor || !b.kmajor) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: split-K products take k-major operands");
+    GemmArgs& args = *out;
+    args = GemmArgs{};
     args.a = a;
     args.b = b;
     args.m = m;
@@ -651,7 +691,38 @@ int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOp
     args.want_colsum = want_colsum ? 1 : 0;
     args.z_off = z_off;
     args.ksplit_total = ksplit_total;
-    return launch_gemm<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k), stream);
+    finish_args<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k));
+    return 0;
+}
+}  // namespace
+
+int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum,
+                         float* partial, int ksplit, int z_off, int ksplit_total, hipStream_t stream) {
+    GemmArgs args;
+    RKA_RETURN_IF_ERR(split_args(m, n, k, a, b, want_colsum, partial, ksplit, z_off, ksplit_total, &args));
+    return launch_gemm<true>(args, ksplit, args.a_vec != 0, args.b_vec != 0, stream);
+}
+
+int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream) {
+    GemmArgs a0, a1;
+    RKA_RETURN_IF_ERR(split_args(p0.m, p0.n, p0.k, p0.a, p0.b, p0.colsum != nullptr, p0.partial, p0.ksplit, 0,
+                                 p0.ksplit, &a0));
+    RKA_RETURN_IF_ERR(split_args(p1.m, p1.n, p1.k, p1.a, p1.b, p1.colsum != nullptr, p1.partial, p1.ksplit, 0,
+                                 p1.ksplit, &a1));
+    if (p1.b.shift_T > 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: only the first product of a pair is remapped");
+    const bool seg = a0.a.seg.len || a0.b.seg.len || a1.a.seg.len || a1.b.seg.len;
+    if (seg) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: pair products take whole operands");
+    const dim3 grid(a0.tiles * a0.ksplit + a1.tiles * a1.ksplit);
+    if (p0.b.shift_T > 0)
+        hipLaunchKernelGGL((gemm_f32_pair_kernel<true, false>), grid, dim3(NT), 0, stream, a0, a1);
+    else
+        hipLaunchKernelGGL((gemm_f32_pair_kernel<false, false>), grid, dim3(NT), 0, stream, a0, a1);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+int splitk_reduce(const SplitProduct& p, hipStream_t stream) {
+    return splitk_reduce(p.m, p.n, p.partial, p.ksplit, p.rot, p.c, p.ldc, p.colsum, stream);
 }
 
 int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,
@@ -663,13 +734,6 @@ int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot,
                        rot, c, ldc, colsum, vec);
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
-}
-
-int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
-                float* c, int ldc, float* colsum, int rot,
-                float* partial, int ksplit, hipStream_t stream) {
-    RKA_RETURN_IF_ERR(gemm_splitk_partials(m, n, k, a, b, colsum != nullptr, partial, ksplit, 0, ksplit, stream));
-    return splitk_reduce(m, n, partial, ksplit, rot, c, ldc, colsum, stream);
 }
 
 }  // namespace rka

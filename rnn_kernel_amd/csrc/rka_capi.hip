@@ -106,9 +106,12 @@ BwdLayout bwd_layout(int B, int T, int I, int H) {
     BwdLayout l{};
     l.nc = backward_chunks(T);
     const int Kc = B * chunk_len(T, l.nc, 0);
-    const int wgs = l.nc > 1 ? 0 : 3;  // resident split-K workgroups per CU
-    l.ks_hh = choose_ksplit(3 * H, H, Kc, 256, wgs);
-    l.ks_ih = choose_ksplit(3 * H, I, Kc, 256, wgs);
+    // resident split-K workgroups per CU; unchunked, the two products share
+    // one launch (gemm_splitk_pair), so each is sized for half the CUs
+    const int wgs = l.nc > 1 ? 0 : 3;
+    const int cus = l.nc > 1 ? 256 : 128;
+    l.ks_hh = choose_ksplit(3 * H, H, Kc, cus, wgs);
+    l.ks_ih = choose_ksplit(3 * H, I, Kc, cus, wgs);
     l.g = 0;
     l.rec = align_up((size_t)B * T * 4 * H * sizeof(float), 256);
     l.part_hh = l.rec + align_up(rec_workspace_bytes(B, H), 256);
@@ -144,7 +147,7 @@ int side_stream(int dev, SideStream** out) {
 
 // ------------------------------------------------------ stage profiler ---
 const char* const kStageNames[RKA_NUM_STAGES] = {"input_gemm", "forward_recurrence", "backward_recurrence",
-                                                 "dw_hh_gemm", "dw_ih_gemm", "dx_gemm"};
+                                                 "dw_gemm", "dw_reduce", "dx_gemm"};
 struct ProfRecord {
     int stage;
     hipEvent_t start, stop;
@@ -223,15 +226,12 @@ int backward_chunked(const float* x, const float* h0, const float* w_ih, const f
         const int Kc = B * L;
         GemmOperand gh{g, 4 * H, 1, 0, nullptr, seg};
         GemmOperand hprev{y, H, 1, T, h0, seg};
+        GemmOperand gi{g + H, 4 * H, 1, 0, nullptr, seg};
+        GemmOperand xk{x, I, 1, 0, nullptr, seg};
         {
             StageScope scope(3, side);
             RKA_RETURN_IF_ERR(gemm_splitk_partials(3 * H, H, Kc, gh, hprev, true, part_hh, l.ks_hh, c * l.ks_hh,
                                                    l.nc * l.ks_hh, side));
-        }
-        GemmOperand gi{g + H, 4 * H, 1, 0, nullptr, seg};
-        GemmOperand xk{x, I, 1, 0, nullptr, seg};
-        {
-            StageScope scope(4, side);
             RKA_RETURN_IF_ERR(gemm_splitk_partials(3 * H, I, Kc, gi, xk, true, part_ih, l.ks_ih, c * l.ks_ih,
                                                    l.nc * l.ks_ih, side));
         }
@@ -244,11 +244,8 @@ int backward_chunked(const float* x, const float* h0, const float* w_ih, const f
         t_hi = t_lo;
     }
     {
-        StageScope scope(3, side);
-        RKA_RETURN_IF_ERR(splitk_reduce(3 * H, H, part_hh, l.nc * l.ks_hh, H, dw_hh, H, db_hh, side));
-    }
-    {
         StageScope scope(4, side);
+        RKA_RETURN_IF_ERR(splitk_reduce(3 * H, H, part_hh, l.nc * l.ks_hh, H, dw_hh, H, db_hh, side));
         RKA_RETURN_IF_ERR(splitk_reduce(3 * H, I, part_ih, l.nc * l.ks_ih, 0, dw_ih, I, db_ih, side));
     }
     RKA_RETURN_IF_HIP(hipEventRecord(ss->ev[l.nc], side));
@@ -353,21 +350,20 @@ int rka_gru_backward(const float* x, const float* h0, const float* w_ih, const f
                                               l.part_hh - l.rec, B, T, H, s));
     }
     const int K = B * T;
-    // dW_hh = G_h^T Hprev, G_h = g[:, 0:3H] in (n, r, z) order -> rotate rows by H.
-    GemmOperand gh{g, 4 * H, 1, 0, nullptr};
-    GemmOperand hprev{y, H, 1, T, h0};
+    // dW_hh = G_h^T Hprev, G_h = g[:, 0:3H] in (n, r, z) order -> rotate rows by H;
+    // dW_ih = G_i^T X, G_i = g[:, H:4H] in (r, z, n) order.  One launch.
     {
-        StageScope scope(3, s);
-        RKA_RETURN_IF_ERR(gemm_splitk(3 * H, H, K, gh, hprev, dw_hh, H, db_hh, H,
-                                      reinterpret_cast<float*>(ws + l.part_hh), l.ks_hh, s));
-    }
-    // dW_ih = G_i^T X, G_i = g[:, H:4H] in (r, z, n) order.
-    GemmOperand gi{g + H, 4 * H, 1, 0, nullptr};
-    GemmOperand xk{x, I, 1, 0, nullptr};
-    {
+        const SplitProduct hh{3 * H, H, K, GemmOperand{g, 4 * H, 1, 0, nullptr}, GemmOperand{y, H, 1, T, h0},
+                              dw_hh, H, db_hh, H, reinterpret_cast<float*>(ws + l.part_hh), l.ks_hh};
+        const SplitProduct ih{3 * H, I, K, GemmOperand{g + H, 4 * H, 1, 0, nullptr}, GemmOperand{x, I, 1, 0, nullptr},
+                              dw_ih, I, db_ih, 0, reinterpret_cast<float*>(ws + l.part_ih), l.ks_ih};
+        {
+            StageScope scope(3, s);
+            RKA_RETURN_IF_ERR(gemm_splitk_pair_partials(hh, ih, s));
+        }
         StageScope scope(4, s);
-        RKA_RETURN_IF_ERR(gemm_splitk(3 * H, I, K, gi, xk, dw_ih, I, db_ih, 0,
-                                      reinterpret_cast<float*>(ws + l.part_ih), l.ks_ih, s));
+        RKA_RETURN_IF_ERR(splitk_reduce(hh, s));
+        RKA_RETURN_IF_ERR(splitk_reduce(ih, s));
     }
     if (dx) {
         // dX = G_i W_ih: A(m=bt, k=j) = g[bt, H+j]; B(n=i, k=j) = W_ih[j, i].

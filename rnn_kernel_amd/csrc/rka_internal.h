@@ -82,14 +82,28 @@ int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOp
 int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,
                   float* colsum, hipStream_t stream);
 
-// Split-K product with deterministic reduction.  Output rows are rotated:
+// Split-K products reduce deterministically.  Output rows are rotated:
 // out[o] = C[(o + rot) % m] (rot = 0: no rotation).  colsum (nullable)
-// receives sum_k A(m,k) with the same rotation.  partial must hold
-// splitk_partial_floats(m, n, ksplit) floats.
-int gemm_splitk(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
-                float* c, int ldc, float* colsum, int rot,
-                float* partial, int ksplit, hipStream_t stream);
+// receives sum_k A(m,k) with the same rotation.  A partial buffer of
+// ksplit slices holds splitk_partial_floats(m, n, ksplit) floats.
 size_t splitk_partial_floats(int m, int n, int ksplit);
+// One product of gemm_splitk_pair_partials.
+struct SplitProduct {
+    int m, n, k;
+    GemmOperand a, b;
+    float* c;
+    int ldc;
+    float* colsum;
+    int rot;
+    float* partial;
+    int ksplit;
+};
+// The partial products of two split-K products in one launch (all slices
+// of each; reduce each with splitk_reduce); only p0's B operand may carry
+// the row remap.  With the reductions, the same results as two gemm_splitk
+// calls with the same slices.
+int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream);
+int splitk_reduce(const SplitProduct& p, hipStream_t stream);
 // Slices for a split-K product of about wgs_per_cu workgroups per CU
 // (0: half a workgroup per CU, for products that share the GPU with a
 // concurrently running recurrence); a multiple of 8 from 8 up.
