@@ -118,6 +118,133 @@ def time_steps(model, x, h0, target, steps, warmup, sync, profile_cb=None, loss_
     return elapsed / steps
 
 
+# The other BASELINE configs, measured with `--workload` (the default run is c2
+# and keeps the one-line contract above; these print one JSON line each too).
+OTHER_WORKLOADS = {
+    # hidden sweep, I = H, B = 64, T = 512
+    "c3": [dict(L=1, I=h, H=h, B=64, T=512, h0_scale=0.1) for h in (64, 96, 128, 129, 130, 160, 192)],
+    # two stacked layers
+    "c4": [dict(L=2, I=256, H=256, B=256, T=1024, h0_scale=0.1)],
+    # 8 chunks of 512 carrying h without detach (gradients flow through all chunks)
+    "c5": [dict(L=1, I=128, H=256, B=16, T=4096, h0_scale=0.5, chunks=8, saturate=True)],
+    # the same with the carried state detached (truncated BPTT: a backward per chunk)
+    "c5-detached": [dict(L=1, I=128, H=256, B=16, T=4096, h0_scale=0.5, chunks=8, saturate=True, detach=True)],
+    # c2 forward only, no autograd (the inference path: no gate cache)
+    "infer": [dict(L=1, I=256, H=256, B=64, T=512, h0_scale=0.1, infer=True)],
+}
+
+
+def workload_inputs(w):
+    import torch
+
+    torch.manual_seed(SEED)
+    gru = torch.nn.GRU(w["I"], w["H"], num_layers=w["L"], batch_first=True)
+    x = torch.randn(w["B"], w["T"], w["I"])
+    if w.get("saturate"):
+        # 5 % of the [B, T] rows of x scaled x10 (gate saturation)
+        g = torch.Generator().manual_seed(SEED + 1)
+        mask = torch.rand(w["B"], w["T"], generator=g) < 0.05
+        x = torch.where(mask[..., None], x * 10.0, x)
+    h0 = w["h0_scale"] * torch.randn(w["L"], w["B"], w["H"])
+    target = torch.randn(w["B"], w["T"], w["H"])
+    return gru, x, h0, target
+
+
+def time_workload(model, w, x, h0, target, steps, warmup, sync, loss_fn):
+    """Mean seconds of one step of workload w: forward over the chunks, MSE
+    loss and backward (per chunk when the carried state is detached), or the
+    forward alone without autograd for the inference workload."""
+    import torch
+
+    chunks = w.get("chunks", 1)
+
+    def step():
+        if w.get("infer"):
+            with torch.no_grad():
+                model(x, h0)
+            return
+        for p in model.parameters():
+            p.grad = None
+        x.grad = None
+        h0.grad = None
+        if chunks == 1:
+            out, _ = model(x, h0)
+            loss_fn(out, target).backward()
+            return
+        hidden = h0
+        outs = []
+        for xc, tc in zip(x.chunk(chunks, dim=1), target.chunk(chunks, dim=1)):
+            if w.get("detach"):
+                out, hidden = model(xc, hidden.detach())
+                loss_fn(out, tc).backward()
+            else:
+                out, hidden = model(xc, hidden)
+                outs.append(out)
+        if outs:
+            loss_fn(torch.cat(outs, dim=1), target).backward()
+
+    for _ in range(warmup):
+        step()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sync()
+    return (time.perf_counter() - t0) / steps
+
+
+def run_other_workload(name, args):
+    import torch
+    import torch.nn.functional as F
+
+    from rnn_kernel_amd import from_torch_gru, mse_loss
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    sync = torch.cuda.synchronize
+    rows = []
+    for w in OTHER_WORKLOADS[name]:
+        gru, x_cpu, h0_cpu, target_cpu = workload_inputs(w)
+        grad = not w.get("infer")
+        x = x_cpu.to(dev).requires_grad_(grad)
+        h0 = h0_cpu.to(dev).requires_grad_(grad)
+        target = target_cpu.to(dev)
+        gru = gru.to(dev)
+        ours = from_torch_gru(gru)
+        t_ours = time_workload(ours, w, x, h0, target, args.steps, args.warmup, sync, mse_loss)
+        row = {k: w[k] for k in ("L", "I", "H", "B", "T")}
+        row.update({"ms_per_step": t_ours * 1e3, "timesteps_per_s": w["T"] / t_ours,
+                    "us_per_timestep": t_ours * 1e6 / w["T"], "tokens_per_s": w["B"] * w["T"] / t_ours})
+        if not args.skip_torch_gpu:
+            gru.flatten_parameters()
+            t_torch = time_workload(gru, w, x, h0, target, max(3, args.steps // 2), 2, sync, F.mse_loss)
+            row["torch_gru_gpu_ms_per_step"] = t_torch * 1e3
+            row["speedup_of_ours"] = t_torch / t_ours
+        rows.append(row)
+        del ours, gru, x, h0, target
+        torch.cuda.empty_cache()
+    first = OTHER_WORKLOADS[name][0]
+    kind = "forward only, no autograd" if first.get("infer") else "fwd+bwd, MSE loss, no optimizer"
+    if first.get("chunks"):
+        kind += f", {first['chunks']} chunks carrying h" + (" (detached)" if first.get("detach") else "")
+    result = {
+        "metric": f"fp32 GRU {kind}: timesteps/s and µs/timestep, 1 MI355X",
+        "workload": name,
+        "unit": "timesteps/s",
+        "value": rows[0]["timesteps_per_s"] if len(rows) == 1 else None,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "higher_is_better": True,
+        "dtype": "fp32",
+        "data": "synthetic (seed 42, CPU-generated, PyTorch-uniform init)",
+        "results": rows,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def cpu_oracle_baseline(budget_s: float):
     """C oracle (fp32, single thread) on the c2 shape with fewer timesteps."""
     import numpy as np
@@ -182,11 +309,17 @@ def main():
                              "the next one fits")
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-torch-gpu", action="store_true")
+    parser.add_argument("--workload", default="c2", choices=["c2"] + sorted(OTHER_WORKLOADS),
+                        help="c2 (default): the headline line; the others measure the remaining BASELINE configs "
+                             "and the inference path, ours and torch.nn.GRU on the same GPU")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path is single-GPU "
               "and its data-parallel sharding is a design note, not a measured configuration.", file=sys.stderr)
         sys.exit(2)
+    if args.workload != "c2":
+        run_other_workload(args.workload, args)
+        return
 
     import torch
 
@@ -246,6 +379,8 @@ def main():
         "tokens_per_s": B * T / t_step,
         "step_tflops": flops_per_step(B, T, I, H) / t_step / 1e12,
         "stages_ms": {k: round(v, 4) for k, v in stage_step.items()},
+        "recurrence_us_per_timestep": {"forward": stage_step.get("forward_recurrence", 0.0) * 1e3 / T,
+                                       "backward": stage_step.get("backward_recurrence", 0.0) * 1e3 / T},
         "launches_per_step": {k: round(v, 2) for k, v in launches.items()},
         "roofline": {
             "kernel": dominant,

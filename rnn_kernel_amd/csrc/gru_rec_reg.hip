@@ -330,31 +330,35 @@ __global__ __launch_bounds__(NTH) void gru_fwd_reg_kernel(
     }
 }
 
-// Forward recurrence for one batch row per workgroup at 193 <= H <= 256
-// (four slices) with the workgroup's own slice of h_{t-1} taken from LDS.
+// Forward recurrence for one batch row per workgroup, S = ceil(H / 64)
+// slices of 64 units (one workgroup each), with the workgroup's own slice of
+// h_{t-1} taken from LDS (S = 1: no exchange at all).
 // Wavefront w takes units 32 (w / 4) + l % 32 of the slice and k quarter
 // Q = w % 4: its half hf = l / 32 holds, for each slot j (slot 0 = its own
-// slice, slots 1..3 = the other three in rotation), the eight k =
-// 64 ((s + j) mod 4) + 16 Q + 8 hf + i of the unit's three W_hh rows.  The
+// slice, slots 1..S-1 = the others in rotation), the eight k =
+// 64 ((s + j) mod S) + 16 Q + 8 hf + i of the unit's three W_hh rows.  The
 // two halves' sums are added with a permlane swap, so each unit and gate
 // has four wave partials to reduce (eight when every wave took all 64
 // units: forward 0.481 vs 0.472 ms per launch).  After the owner publishes h_t it also writes
 // it to LDS; a second barrier follows and every wavefront runs the own
 // slot's 24 FMAs of step t+1 while the other slices' words are still on
 // their way, leaving 72 FMAs per lane after they arrive (96 with the whole
-// chunk polled).  The h values reach the FMAs as wave-uniform VGPRs read
+// chunk polled; at S = 4).  The h values reach the FMAs as wave-uniform VGPRs read
 // from LDS (broadcast ds_read_b128): the polled words are written to a
 // wave-private LDS row first.  Measured on MI355X, a VGPR-operand v_fmac_f32
 // issues at ~1.2 ns per SIMD with two waves per SIMD against ~2.0 ns for
 // the row-broadcast DPP form and ~2.1 ns with an SGPR operand.
+template <int S>
 __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
     const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
     float* __restrict__ reserve, unsigned long long* __restrict__ exch, int* __restrict__ abort_flag,
     RegParams p) {
+    constexpr int NR = S - 1;              // remote slots
+    constexpr int NP = NR > 0 ? 8 * NR : 4;  // polled h values per wave half
     __shared__ float part[2][4][3][64];  // [step parity][k quarter][gate][unit]
     __shared__ __attribute__((aligned(16))) float hloc[2][64];
-    __shared__ __attribute__((aligned(16))) float hrem[NW][2][24];  // per wave and half: 24 polled h values
+    __shared__ __attribute__((aligned(16))) float hrem[NW][2][NP];  // per wave and half: the polled h values
     __shared__ int s_abort;
 
     const int B = p.B, T = p.T, H = p.H;
@@ -372,14 +376,14 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     const int fu = 32 * (wave >> 2) + uu;  // the lane's FMA unit within the slice
     const int uf = s * 64 + fu;
     const bool ufvalid = uf < H;
-    auto kofh = [&](int half, int j, int i) { return 64 * ((s + j) & 3) + 16 * Q + 8 * half + i; };
+    auto kofh = [&](int half, int j, int i) { return 64 * ((s + j) % S) + 16 * Q + 8 * half + i; };
     auto kof = [&](int j, int i) { return kofh(hf, j, i); };
 
     // slot j's W_hh entries in w?[8 j .. 8 j + 7]
-    float wr[32], wz[32], wn[32];
+    float wr[8 * S], wz[8 * S], wn[8 * S];
     const bool vec = p.wvec != 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < S; ++j) {
 #pragma unroll
         for (int i = 0; i < 8; i += 4) {
             const int k = kof(j, i);
@@ -433,17 +437,17 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     __shared__ int s_local;
     const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
 
-    // Lane l < 48 polls half l / 24, slot 1 + (l % 24) / 8, entry l % 8;
+    // Lane l < 2 NP polls half l / NP, slot 1 + (l % NP) / 8, entry l % 8;
     // other lanes, and lanes of a k past H, re-read the wave's first valid
-    // remote word.
-    auto pkof = [&](int l) { return kofh(l / 24, 1 + (l % 24) / 8, l % 8); };
+    // remote word (word 0 when it has none).
+    auto pkof = [&](int l) { return kofh(l / NP, 1 + (l % NP) / 8, l % 8); };
     int fallback = -1;
 #pragma unroll
-    for (int l = 0; l < 48; ++l) {
+    for (int l = 0; l < 2 * NP * (NR > 0); ++l) {
         const int k = pkof(l);
         if (fallback < 0 && k < H) fallback = k;
     }
-    const int pk = lane < 48 ? pkof(lane) : H;
+    const int pk = NR > 0 && lane < 2 * NP ? pkof(lane) : H;
     const bool pvalid = pk < H;
     const int pidx = pvalid ? pk : (fallback >= 0 ? fallback : 0);
 
@@ -496,36 +500,36 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     }
     auto step = [&](int t, const float (&cur)[3], float (&nxt)[3]) -> bool {
         // @probe:step_begin
-        float hx;
-        if (t == 0) {
-            hx = pvalid ? h0[(size_t)row * H + pidx] : 0.f;
-        } else {
-            const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H + (size_t)row * H;
-            const unsigned long long* pp[1] = {src + pidx};
-            const bool pv[1] = {pvalid};
-            unsigned long long w[1] = {first_read};
-            bool ok = true;
-            rec::wait_words<1>(pp, pv, w, (unsigned)t, abort_flag, ok);
-            hx = pvalid ? __uint_as_float((unsigned)w[0]) : 0.f;
-            if (!ok) s_abort = 1;
+        float hv[NR > 0 ? NR : 1][8];
+        if constexpr (NR > 0) {
+            float hx;
+            if (t == 0) {
+                hx = pvalid ? h0[(size_t)row * H + pidx] : 0.f;
+            } else {
+                const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H + (size_t)row * H;
+                const unsigned long long* pp[1] = {src + pidx};
+                const bool pv[1] = {pvalid};
+                unsigned long long w[1] = {first_read};
+                bool ok = true;
+                rec::wait_words<1>(pp, pv, w, (unsigned)t, abort_flag, ok);
+                hx = pvalid ? __uint_as_float((unsigned)w[0]) : 0.f;
+                if (!ok) s_abort = 1;
+            }
+            // lanes 0..NP-1 hold slot 1 + l / 8, entry l % 8 of half 0 (NP..
+            // of half 1): through the wave's LDS row to every lane (one wave
+            // writes and reads the row; LDS keeps a wave's accesses in order)
+            if (lane < 2 * NP) hrem[wave][lane / NP][lane % NP] = hx;
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][hf][8 * jj], hv[jj]);
         }
-        // lanes 0..23 hold slot 1 + l / 8, entry l % 8: through the wave's
-        // LDS row to every lane (one wave writes and reads the row; LDS
-        // keeps a wave's accesses in order)
-        if (lane < 48) hrem[wave][lane / 24][lane % 24] = hx;
-        __builtin_amdgcn_wave_barrier();
-        float hv1[8], hv2[8], hv3[8];
-        lds8(&hrem[wave][hf][0], hv1);
-        lds8(&hrem[wave][hf][8], hv2);
-        lds8(&hrem[wave][hf][16], hv3);
         if (owner) {
             if (t > 0) store_outputs(t - 1);
             if (t + 1 < T) load_gx(nxt, t + 1);
         }
         // @probe:polled
-        fma8(hv1, 1);
-        fma8(hv2, 2);
-        fma8(hv3, 3);
+#pragma unroll
+        for (int jj = 0; jj < NR; ++jj) fma8(hv[jj], jj + 1);
         {
             // halves: lanes 0-31 get the r sum and lanes 32-63 the z sum of
             // unit fu, every lane the n sum (lower half + upper half)
@@ -551,8 +555,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
             const float z = rec::sigmoid_f(cur[1] + sz);
             const float n = rec::tanh_f(cur[2] + r * sn);
             const float h = n + z * (h_prev - n);
-            rec::publish_word(exch + (size_t)(t & 1) * B * H + (size_t)row * H + u,
-                              rec::pack_word(h, (unsigned)(t + 1)), xlocal);
+            if constexpr (NR > 0)
+                rec::publish_word(exch + (size_t)(t & 1) * B * H + (size_t)row * H + u,
+                                  rec::pack_word(h, (unsigned)(t + 1)), xlocal);
             o_h = h;
             o_r = r;
             o_z = z;
@@ -566,10 +571,10 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         // the own slot of step t+1 while the other slices' words travel,
         // with the first poll read of step t+1 already in flight
         if (t + 1 < T) {
-            first_read = rec::load_word(exch + (size_t)(t & 1) * B * H + (size_t)row * H + pidx);
-            float hv[8];
-            lds8(&hloc[t & 1][16 * Q + 8 * hf], hv);
-            local_fmas(hv);
+            if constexpr (NR > 0) first_read = rec::load_word(exch + (size_t)(t & 1) * B * H + (size_t)row * H + pidx);
+            float hl[8];
+            lds8(&hloc[t & 1][16 * Q + 8 * hf], hl);
+            local_fmas(hl);
         }
         // @probe:step_end
         return !abort_now;
@@ -785,13 +790,14 @@ __device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
-// Backward recurrence for one batch row per workgroup at 193 <= H <= 256
-// (four slices) with the workgroup's own G_h words taken from LDS.
+// Backward recurrence for one batch row per workgroup, S = ceil(H / 64)
+// slices, with the workgroup's own G_h words taken from LDS.
 // The 3H G_h words of a step are split into the workgroup's own 192 (gate
-// c, unit m of its slice at index e = 64 c + m) and 576 remote ones (flat
-// index r: slot 1 + r / 192 of the other slices in rotation, then e).  The
-// workgroup's 32 sixteen-lane rows are j-groups: row J = 4 w + rho of wave w
-// takes own entries 6 J .. 6 J + 5 and remote entries 18 J .. 18 J + 17, and
+// c, unit m of its slice at index e = 64 c + m) and 192 (S - 1) remote ones
+// (flat index r: slot 1 + r / 192 of the other slices in rotation, then e).
+// The workgroup's 32 sixteen-lane rows are j-groups: row J = 4 w + rho of
+// wave w takes own entries 6 J .. 6 J + 5 and remote entries RE J ..
+// RE J + RE - 1 (RE = 6 (S - 1)), and
 // lane q of the row takes units 64 s + 4 q .. 4 q + 3, so every G value
 // feeds four FMAs of a lane.  The G values reach the FMAs as VGPRs uniform
 // over a row (ds_read_b128 from LDS, one address per row): plain v_fmac_f32
@@ -805,14 +811,18 @@ __device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
 // runs the next step's pointwise math, publishes its G words and writes
 // them to LDS; after a second barrier every wave runs the own entries' FMAs
 // while the other slices' words travel.
+template <int S>
 __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
     const float* __restrict__ h0, const float* __restrict__ y, const float* __restrict__ w_hh,
     float* __restrict__ gout, float* __restrict__ dh0, unsigned long long* __restrict__ exch,
     int* __restrict__ abort_flag, RegParams p) {
+    constexpr int RE = 6 * (S - 1);                  // remote entries per j-group
+    constexpr int WE = 4 * RE;                       // remote entries polled per wave
+    constexpr int GR = RE > 0 ? (RE + 3) / 4 * 4 : 4;  // LDS row of a j-group's polled words
     __shared__ __attribute__((aligned(16))) float part[2][NW][64];
     __shared__ __attribute__((aligned(16))) float gloc[32][8];      // own G words by j-group (6 used)
-    __shared__ __attribute__((aligned(16))) float grem[NW][4][20];  // per wave: polled words by row (18 used)
+    __shared__ __attribute__((aligned(16))) float grem[NW][4][GR];  // per wave: polled words by row
     __shared__ int s_abort;
 
     const int B = p.B, T = p.T, H = p.H;
@@ -834,13 +844,13 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         return (e >> 6) * H + 64 * s + m;
     };
     auto rem_row = [&](int r, bool& valid) {
-        const int e = r % 192, m = e & 63, sl = (s + 1 + r / 192) & 3;
+        const int e = r % 192, m = e & 63, sl = (s + 1 + r / 192) % S;
         valid = 64 * sl + m < H;
         return (e >> 6) * H + 64 * sl + m;
     };
 
     // W_hh[j][ub .. ub + 3] for the row's own (wl) and remote (wm) entries
-    float wl[6][4], wm[18][4];
+    float wl[6][4], wm[RE > 0 ? RE : 1][4];
     const bool vec = p.wvec != 0;
     auto load4 = [&](int jr, bool ok, float (&d)[4]) {
         const float* src = w_hh + (size_t)jr * H + ub;
@@ -862,9 +872,9 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         load4(jr, ok, wl[i]);
     }
 #pragma unroll
-    for (int i = 0; i < 18; ++i) {
+    for (int i = 0; i < RE; ++i) {
         bool ok;
-        const int jr = rem_row(18 * J + i, ok);
+        const int jr = rem_row(RE * J + i, ok);
         load4(jr, ok, wm[i]);
     }
 
@@ -896,23 +906,23 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     __shared__ int s_local;
     const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
 
-    // Wave w polls remote entries 72 w .. 72 w + 71: register 0 lane l entry
-    // 72 w + l, register 1 lane l entry 72 w + 64 + l % 8.  Lanes without a
-    // word re-read the register's first valid word (else the wave's first
-    // valid remote word, else word 0).
+    // Wave w polls remote entries WE w .. WE w + WE - 1: register 0 lane l
+    // entry WE w + l (l < WE), register 1 (S = 4: WE = 72) lane l entry
+    // WE w + 64 + l % 8.  Lanes without a word re-read the register's first
+    // valid word (else the wave's first valid remote word, else word 0).
     int first_any = -1, first1 = -1;
 #pragma unroll
-    for (int e = 0; e < 72; ++e) {
+    for (int e = 0; e < WE; ++e) {
         bool ok;
-        const int jr = rem_row(72 * wave + e, ok);
+        const int jr = rem_row(WE * wave + e, ok);
         if (ok && first_any < 0) first_any = jr;
         if (ok && e >= 64 && first1 < 0) first1 = jr;
     }
     if (first_any < 0) first_any = 0;
     if (first1 < 0) first1 = first_any;
-    bool pv0, pv1;
-    int pidx0 = rem_row(72 * wave + lane, pv0);
-    int pidx1 = rem_row(72 * wave + 64 + (lane & 7), pv1);
+    bool pv0 = false, pv1 = false;
+    int pidx0 = lane < WE ? rem_row(WE * wave + lane, pv0) : 0;
+    int pidx1 = WE > 64 ? rem_row(WE * wave + 64 + (lane & 7), pv1) : 0;
     if (!pv0) pidx0 = first_any;
     if (!pv1) pidx1 = first1;
 
@@ -929,12 +939,14 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
             o_drh = o_dnh * ca * cr * (1.0f - cr);
             o_dzh = dz * cz * (1.0f - cz);
             ddirect = gsum * cz;
-            const unsigned tag = (unsigned)(i + 1);
-            unsigned long long* wp = exch + (size_t)(i & 1) * B * H3 + (size_t)row * H3 + u;
-            unsigned long long* const pp3[3] = {wp, wp + H, wp + 2 * H};
-            const unsigned long long w3[3] = {rec::pack_word(o_drh, tag), rec::pack_word(o_dzh, tag),
-                                              rec::pack_word(o_dan, tag)};
-            rec::publish_words<3>(pp3, w3, xlocal);
+            if constexpr (RE > 0) {
+                const unsigned tag = (unsigned)(i + 1);
+                unsigned long long* wp = exch + (size_t)(i & 1) * B * H3 + (size_t)row * H3 + u;
+                unsigned long long* const pp3[3] = {wp, wp + H, wp + 2 * H};
+                const unsigned long long w3[3] = {rec::pack_word(o_drh, tag), rec::pack_word(o_dzh, tag),
+                                                  rec::pack_word(o_dan, tag)};
+                rec::publish_words<3>(pp3, w3, xlocal);
+            }
         }
         if (wave == 0) {
             const float gv[3] = {owner ? o_drh : 0.f, owner ? o_dzh : 0.f, owner ? o_dan : 0.f};
@@ -965,8 +977,8 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     unsigned long long first_read[2] = {0, 0};
     auto first_poll = [&](int i) {
         const unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3 + (size_t)row * H3;
-        first_read[0] = rec::load_word(slotp + pidx0);
-        first_read[1] = rec::load_word(slotp + pidx1);
+        if constexpr (WE > 0) first_read[0] = rec::load_word(slotp + pidx0);
+        if constexpr (WE > 64) first_read[1] = rec::load_word(slotp + pidx1);
     };
     // one timestep (i-th from the end): its G words are published and its
     // own-entry FMAs done; false when the workgroup must stop
@@ -974,31 +986,39 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         // @probe:step_begin
         const int t = T - 1 - i;
         const unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3 + (size_t)row * H3;
-        float gr0, gr1;
-        {
-            const unsigned long long* pp[2] = {slotp + pidx0, slotp + pidx1};
-            const bool pv[2] = {pv0, pv1};
-            unsigned long long wd[2] = {first_read[0], first_read[1]};
+        float g[GR];
+        if constexpr (WE > 0) {
+            float gr0, gr1 = 0.f;
             bool ok = true;
-            rec::wait_words<2>(pp, pv, wd, (unsigned)(i + 1), abort_flag, ok);
-            gr0 = pv0 ? __uint_as_float((unsigned)wd[0]) : 0.f;
-            gr1 = pv1 ? __uint_as_float((unsigned)wd[1]) : 0.f;
+            if constexpr (WE > 64) {
+                const unsigned long long* pp[2] = {slotp + pidx0, slotp + pidx1};
+                const bool pv[2] = {pv0, pv1};
+                unsigned long long wd[2] = {first_read[0], first_read[1]};
+                rec::wait_words<2>(pp, pv, wd, (unsigned)(i + 1), abort_flag, ok);
+                gr0 = pv0 ? __uint_as_float((unsigned)wd[0]) : 0.f;
+                gr1 = pv1 ? __uint_as_float((unsigned)wd[1]) : 0.f;
+            } else {
+                const unsigned long long* pp[1] = {slotp + pidx0};
+                const bool pv[1] = {pv0};
+                unsigned long long wd[1] = {first_read[0]};
+                rec::wait_words<1>(pp, pv, wd, (unsigned)(i + 1), abort_flag, ok);
+                gr0 = pv0 ? __uint_as_float((unsigned)wd[0]) : 0.f;
+            }
             if (!ok) s_abort = 1;
-        }
-        // polled entry e of the wave to row e / 18, position e % 18 of its LDS
-        // block (one wave writes and reads the block; LDS keeps a wave's
-        // accesses in order)
-        grem[wave][lane / 18][lane % 18] = gr0;
-        if (lane < 8) grem[wave][(64 + lane) / 18][(64 + lane) % 18] = gr1;
-        __builtin_amdgcn_wave_barrier();
-        float g[20];
+            // polled entry e of the wave to row e / RE, position e % RE of its
+            // LDS block (one wave writes and reads the block; LDS keeps a
+            // wave's accesses in order)
+            if (lane < WE) grem[wave][lane / RE][lane % RE] = gr0;
+            if (WE > 64 && lane < WE - 64) grem[wave][(64 + lane) / RE][(64 + lane) % RE] = gr1;
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int k = 0; k < 5; ++k) {
-            const float4 v = *reinterpret_cast<const float4*>(&grem[wave][rho][4 * k]);
-            g[4 * k] = v.x;
-            g[4 * k + 1] = v.y;
-            g[4 * k + 2] = v.z;
-            g[4 * k + 3] = v.w;
+            for (int k = 0; k < GR / 4; ++k) {
+                const float4 v = *reinterpret_cast<const float4*>(&grem[wave][rho][4 * k]);
+                g[4 * k] = v.x;
+                g[4 * k + 1] = v.y;
+                g[4 * k + 2] = v.z;
+                g[4 * k + 3] = v.w;
+            }
         }
         if (owner) {
             float* op = gout + ((size_t)row * T + t) * 4 * H;
@@ -1009,7 +1029,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
             if (t - 2 >= p.t_begin) load_inputs(cur, t - 2);
         }
         // @probe:polled
-        fma_group(g, 18, wm);
+        if constexpr (RE > 0) fma_group(g, RE, wm);
         float tot[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) tot[v] = acc[0][v] + acc[1][v];
@@ -1075,13 +1095,27 @@ const void* bwd_ptr(int nj) {
     }
 }
 
-const void* kernel_ptr(int dir, int cap, int rows) {
+template <int S>
+const void* local_ptr(int dir) {
+    return dir == 0 ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S>)
+                    : reinterpret_cast<const void*>(&gru_bwd_local_kernel<S>);
+}
+
+// One batch row per workgroup: the local-slice kernels (S slices); more rows:
+// the row-broadcast kernels.
+const void* kernel_ptr(int dir, int cap, int rows, int slices) {
+    if (rows == 1) {
+        switch (slices) {
+            case 1: return local_ptr<1>(dir);
+            case 2: return local_ptr<2>(dir);
+            case 3: return local_ptr<3>(dir);
+            default: return local_ptr<4>(dir);
+        }
+    }
     if (dir == 0) {
-        if (rows == 1) return fwd_ptr<1>(cap);
         if (rows == 2) return fwd_ptr<2>(cap);
         return fwd_ptr<4>(cap);
     }
-    if (rows == 1) return bwd_ptr<1>(cap);
     if (rows == 2) return bwd_ptr<2>(cap);
     return bwd_ptr<4>(cap);
 }
@@ -1114,7 +1148,7 @@ int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_
         if (fixed_rows && rows != fixed_rows) continue;
         const int G = (batch + rows - 1) / rows;
         int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows), NTH, 0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows, S), NTH, 0) != hipSuccess)
             continue;
         if ((long)G * S > (long)per_cu * dev.num_cus) continue;
         cfg->kind = REC_REGISTER;
@@ -1140,10 +1174,7 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
                   (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end,
                   a.xcc_words, a.xcc_tag};
-    const void* k = kernel_ptr(dir, cap, c.rows);
-    if (c.rows == 1 && c.slices == 4)
-        k = dir == 0 ? reinterpret_cast<const void*>(&gru_fwd_local_kernel)
-                     : reinterpret_cast<const void*>(&gru_bwd_local_kernel);
+    const void* k = kernel_ptr(dir, cap, c.rows, c.slices);
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                         (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
