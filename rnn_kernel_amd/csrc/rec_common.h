@@ -239,76 +239,6 @@ __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[
     }
 }
 
-// Row-broadcast FMA: acc += src[16 * (lane / 16) + K] * w on every lane, i.e.
-// lane K of each 16-lane row is broadcast to its row by the DPP operand
-// modifier row_newbcast of the FMA itself.  With the same 16 values held in
-// all four rows this is a wave-wide broadcast that costs no extra
-// instruction (a readlane costs a VALU issue slot, and the VALU write of an
-// SGPR it feeds to the FMA needs wait states).  The compiler does not fold a
-// DPP move into v_fmac_f32, hence the instruction is written out.
-template <int K>
-__device__ __forceinline__ void fma_row_bcast(float& acc, float src, float w) {
-    asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-                 : "+v"(acc)
-                 : "v"(src), "v"(w), "n"(K));
-}
-
-// Row v of a wave-wide vector, replicated into all four 16-lane rows:
-// rows (R0, R1, R2, R3) of x become (Rv, Rv, Rv, Rv) in out[v].
-// v_permlane16_swap exchanges the odd rows of its first operand with the even
-// rows of its second, v_permlane32_swap the upper half of the first with the
-// lower half of the second:
-//   swap16(x, x) -> (R0 R0 R2 R2), (R1 R1 R3 R3)
-//   swap32 of each with itself -> (R0 x4), (R2 x4) and (R1 x4), (R3 x4).
-__device__ __forceinline__ void rows_of(float x, float (&out)[4]) {
-    const unsigned u = __float_as_uint(x);
-    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    const auto q0 = __builtin_amdgcn_permlane32_swap(p[0], p[0], false, false);
-    const auto q1 = __builtin_amdgcn_permlane32_swap(p[1], p[1], false, false);
-    out[0] = __uint_as_float(q0[0]);
-    out[2] = __uint_as_float(q0[1]);
-    out[1] = __uint_as_float(q1[0]);
-    out[3] = __uint_as_float(q1[1]);
-}
-
-// Lane of poll register q whose word lane `lane` loads.  Register q feeds the
-// groups 4 q .. 4 q + 3 (rows 0..3); the lanes of rows no group uses repeat
-// the words of the used rows, so the load instruction still touches only
-// the used words (one request per line, no stand-in address polled by every
-// wave of the grid, no exec-mask branches in the poll loop).
-template <int NV>
-__device__ __forceinline__ int poll_lane(int q, int lane) {
-    const int rows_used = NV - 4 * q < 4 ? NV - 4 * q : 4;
-    return lane % (16 * rows_used);
-}
-
-// Index of the last word of chunk [beg, beg + chunk) below len (word 0 if the
-// chunk is empty): what lanes without a word of their own poll.
-__device__ __forceinline__ int last_valid(int beg, int chunk, int len) {
-    const int end = beg + chunk < len ? beg + chunk : len;
-    return end > beg ? end - 1 : 0;
-}
-
-// Group v (values 16 v .. 16 v + 15 of a chunk held one per lane in
-// x[v / 4][r], lane = value index mod 64) replicated into all rows: out[v][r].
-template <int NV, int NP, int ROWS>
-__device__ __forceinline__ void replicate_rows(const float (&x)[NP][ROWS], int r, float (&out)[NV][ROWS]) {
-#pragma unroll
-    for (int q = 0; q < NP; ++q) {
-        float rows[4];
-        rows_of(x[q][r], rows);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (4 * q + i < NV) out[4 * q + i][r] = rows[i];
-    }
-}
-
-// A DPP operand must not be read within two wait states of the VALU
-// instruction that wrote it; the hazard recogniser does not look inside
-// inline asm.  Routing `src` through this statement orders every producer of
-// src before the wait states and every row-broadcast FMA after them.
-__device__ __forceinline__ void dpp_src_guard(float& src) { asm volatile("s_nop 1" : "+v"(src)); }
-
 }  // namespace rec
 
 // Tiled kernels (W_hh slice in LDS; any hidden size that fits LDS).

@@ -117,6 +117,8 @@ LAYER_SHAPES = [
     (3, 6, 5, 200),      # four slices, the last one partial (float4 weight loads)
     (2, 5, 3, 221),      # four slices, H not a multiple of 4 (scalar weight loads)
     (4, 4, 2, 193),      # four slices, one unit in the last
+    (300, 3, 8, 256),    # B x 4 workgroups not resident: several rows per workgroup, launched in waves
+    (130, 4, 6, 130),    # three slices, two rows per workgroup
 ]
 
 
@@ -153,6 +155,9 @@ def rec_kind(request, hip_lib):
 @pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512)])
 def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
     from rnn_kernel_amd import GRUFunction, _lib
+
+    if rec_kind == "tiled" and B >= 256:
+        pytest.skip("the LDS-tiled recurrences launch resident grids only; this batch needs waves")
 
     print(f"layer vs oracle B={B} T={T} I={I} H={H} kind={rec_kind} "
           f"fwd={_lib.describe_recurrence(0, B, H)} bwd={_lib.describe_recurrence(1, B, H)}", flush=True)
@@ -449,6 +454,41 @@ def test_recurrences_progress_beside_a_concurrent_kernel(gpu, B, H):
         for a, b in zip(solo, busy):
             assert torch.isfinite(b).all()
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("H,fwd_rows,bwd_rows", [(200, 2, 4), (256, 2, 2), (160, 4, 4), (64, 4, 2)])
+def test_rows_per_workgroup_agree(gpu, hip_lib, H, fwd_rows, bwd_rows):
+    """The local-slice recurrences with 2 or 4 batch rows per workgroup
+    (batch 9: the last group partly empty) give the one-row results."""
+    from rnn_kernel_amd import GRU, _lib
+
+    torch.manual_seed(H)
+    model = GRU(16, H).to(gpu)
+    x = torch.randn(9, 7, 16, device=gpu)
+    h0 = 0.3 * torch.randn(1, 9, H, device=gpu)
+
+    def run():
+        model.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        hi = h0.clone().requires_grad_(True)
+        y, hn = model(xi, hi)
+        (y.sin().sum() + hn.sum()).backward()
+        return [y.detach().clone(), hn.detach().clone(), xi.grad.clone(), hi.grad.clone()] + \
+            [p.grad.clone() for p in model.parameters()]
+
+    for d in (0, 1):
+        _lib.set_recurrence_config(d, 2, 0, 1)
+    try:
+        base = run()
+        _lib.set_recurrence_config(0, 2, 0, fwd_rows)
+        _lib.set_recurrence_config(1, 2, 0, bwd_rows)
+        print("rows", _lib.describe_recurrence(0, 9, H), _lib.describe_recurrence(1, 9, H), flush=True)
+        alt = run()
+    finally:
+        for d in (0, 1):
+            _lib.set_recurrence_config(d, 0, 0, 0)
+    for a, b in zip(base, alt):
+        assert _rel(a, b) <= 1e-5
 
 
 @pytest.mark.parametrize("kind,units,param", [(1, 1, 0), (1, 4, 0), (1, 16, 2), (1, 64, 0), (2, 0, 2), (2, 0, 4)])
