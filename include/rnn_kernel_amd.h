@@ -138,13 +138,15 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
 
 /* Override the recurrence kernel choice for direction `dir` (0 forward,
  * 1 backward); affects later calls on all threads.  For tuning and tests.
- * kind 0: automatic (register-resident kernel when hidden_size <= 256 and it
- *         fits resident, else LDS-tiled);
+ * kind 0: automatic (register-resident kernel when hidden_size <= 256, with
+ *         the fewest batch rows per workgroup that make the grid resident,
+ *         else the most, the grid then running in waves; LDS-tiled above);
  * kind 1: LDS-tiled; units = hidden units per workgroup (a divisor of 64,
  *         0 = auto), param = wavefronts holding (row, unit) pairs (1, 2, 4,
  *         0 = auto);
  * kind 2: register-resident; units = 64 (or 0), param = batch rows per
- *         workgroup (1, 2, 4, 0 = auto). */
+ *         workgroup (1, 2, 4, 0 = auto; the forward at hidden_size > 192
+ *         takes at most 2). */
 /* Number of time chunks the backward of a layer runs in (0 = automatic,
  * currently 1; at most 8, and never more than seq_len).  With several chunks
  * the backward recurrence is launched once per time range, latest first,
