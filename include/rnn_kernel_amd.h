@@ -145,8 +145,7 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
  *         0 = auto), param = wavefronts holding (row, unit) pairs (1, 2, 4,
  *         0 = auto);
  * kind 2: register-resident; units = 64 (or 0), param = batch rows per
- *         workgroup (1, 2, 4, 0 = auto; the forward at hidden_size > 192
- *         takes at most 2). */
+ *         workgroup (1, 2, 4, 0 = auto). */
 /* Number of time chunks the backward of a layer runs in (0 = automatic,
  * currently 1; at most 8, and never more than seq_len).  With several chunks
  * the backward recurrence is launched once per time range, latest first,
