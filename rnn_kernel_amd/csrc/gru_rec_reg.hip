@@ -99,7 +99,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
 
     const int B = p.B, T = p.T, H = p.H;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+    const int wave = threadIdx.x >> 6;
     const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
     const int s = gc.s;
     const int row0 = gc.g * R;    // the group's first batch row
