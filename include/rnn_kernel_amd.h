@@ -161,6 +161,17 @@ int rka_set_backward_chunks(int chunks);
  * (-1 on bad arguments). */
 int rka_backward_chunks(int seq_len);
 
+/* Poll rounds a recurrence kernel's wait for another workgroup's words
+ * makes before it gives up (0 = the default, 2^21, also the largest value
+ * accepted).  A wait that gives up raises the launch's abort flag: every
+ * workgroup leaves its time loop, the aborted rows' final states (hn of the
+ * forward, dh0 of the backward) are NaN, and the call itself still returns
+ * 0 (the kernels are asynchronous).  Affects later launches on all threads.
+ * No counterpart in the reference (its recurrence kernels step with
+ * cooperative grid barriers, which wait without a bound); exported so
+ * tests can drive the abort path from the host. */
+int rka_set_spin_limit(int polls);
+
 #define RKA_REC_AUTO 0
 #define RKA_REC_TILED 1
 #define RKA_REC_REGISTER 2

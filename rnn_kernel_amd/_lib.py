@@ -34,6 +34,7 @@ SIGNATURES = {
     "rka_gru_recurrence_backward": (_I, [_P] * 8 + [_P, _SZ, _I, _I, _I, _P]),
     "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
     "rka_set_backward_chunks": (_I, [_I]),
+    "rka_set_spin_limit": (_I, [_I]),
     "rka_backward_chunks": (_I, [_I]),
     "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
     "rka_eval_gate_functions": (_I, [_P, _P, _P, _I, _P]),
@@ -131,6 +132,12 @@ def set_recurrence_config(direction: int, kind: int = 0, units: int = 0, param: 
 def set_backward_chunks(chunks: int) -> None:
     """Time chunks of the backward (0 = automatic); see rka_set_backward_chunks."""
     check(load().rka_set_backward_chunks(chunks), "rka_set_backward_chunks")
+
+
+def set_spin_limit(polls: int) -> None:
+    """Poll rounds a recurrence wait makes before it gives up (0 = default);
+    see rka_set_spin_limit."""
+    check(load().rka_set_spin_limit(polls), "rka_set_spin_limit")
 
 
 def backward_chunks(seq_len: int) -> int:

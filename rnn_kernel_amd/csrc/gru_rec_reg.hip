@@ -60,6 +60,7 @@ struct RegParams {
     int t_begin, t_end;  // backward: time range processed
     unsigned long long* xcc_words;  // start-up XCD check (nullable)
     unsigned xcc_tag;
+    int spin_limit;  // poll rounds before a wait gives up
 };
 
 // Forward recurrence, S = ceil(H / 64) slices of 64 units (one workgroup
@@ -173,7 +174,8 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     }
     if (threadIdx.x == 0) s_abort = 0;
     __shared__ int s_local;
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local,
+                                                   p.spin_limit);
 
     // Lane l < 2 NP polls half l / NP, slot 1 + (l % NP) / 8, entry l % 8 of
     // every row; other lanes, and lanes of a k past H, re-read the wave's
@@ -270,7 +272,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
                     pv[r] = pvalid && rvalid[r];
                 }
                 bool ok = true;
-                rec::wait_words<R>(pp, pv, first_read, (unsigned)t, abort_flag, ok);
+                rec::wait_words<R>(pp, pv, first_read, (unsigned)t, abort_flag, p.spin_limit, ok);
 #pragma unroll
                 for (int r = 0; r < R; ++r) hx[r] = pv[r] ? __uint_as_float((unsigned)first_read[r]) : 0.f;
                 if (!ok) s_abort = 1;
@@ -533,7 +535,8 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     }
     if (threadIdx.x == 0) s_abort = 0;
     __shared__ int s_local;
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local,
+                                                   p.spin_limit);
 
     // Wave w polls remote entries WE w .. WE w + WE - 1 of every row:
     // register 0 lane l entry WE w + l (l < WE), register 1 (S = 4: WE = 72)
@@ -656,7 +659,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
                 }
             }
             bool ok = true;
-            rec::wait_words<NW2 * R>(pp, pv, first_read, (unsigned)(i + 1), abort_flag, ok);
+            rec::wait_words<NW2 * R>(pp, pv, first_read, (unsigned)(i + 1), abort_flag, p.spin_limit, ok);
             if (!ok) s_abort = 1;
             // polled entry e of the wave to row e / RE, position e % RE of its
             // LDS block (one wave writes and reads the blocks; LDS keeps a
@@ -831,7 +834,7 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     const bool aligned = (reinterpret_cast<uintptr_t>(a.w_hh) & 15u) == 0;
     RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
                   (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end,
-                  a.xcc_words, a.xcc_tag};
+                  a.xcc_words, a.xcc_tag, a.spin_limit};
     const void* k = kernel_ptr(dir, cap, c.rows, c.slices);
     if (k == nullptr) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: no kernel for this row count");
     if (dir == 0) {

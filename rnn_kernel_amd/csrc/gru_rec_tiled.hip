@@ -35,13 +35,14 @@ struct RecParams {
     int t_begin, t_end;  // backward: time range processed
     unsigned long long* xcc_words;  // start-up XCD check (nullable)
     unsigned xcc_tag;
+    int spin_limit;  // poll rounds before a wait gives up
 };
 
 // Gathers `nrows` rows of `len` published words with step tag `tag` from
 // src (row stride `len`) into LDS rows of stride RP.  Returns false when the
 // spin budget ran out or another workgroup raised the abort flag.
 __device__ bool gather_rows(const unsigned long long* __restrict__ src, int nrows, int len, unsigned tag,
-                            float* __restrict__ dst, int RP, int* __restrict__ abort_flag) {
+                            float* __restrict__ dst, int RP, int* __restrict__ abort_flag, int spin_limit) {
     using namespace rec;
     const int total = nrows * len;
     bool ok = true;
@@ -59,7 +60,7 @@ __device__ bool gather_rows(const unsigned long long* __restrict__ src, int nrow
             int spins = 0;
             while ((unsigned)(w[j] >> 32) != tag) {
                 if (!ok) break;
-                if (++spins > SPIN_LIMIT) {
+                if (++spins >= spin_limit) {
                     __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     ok = false;
                     break;
@@ -150,13 +151,14 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
     bool aborted = false;
     __shared__ int s_local;
     // the group = the S workgroups of rec::group_coords; plain publishing stores when they share an XCD
-    const bool xlocal = group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal =
+        group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local, p.spin_limit);
     __syncthreads();
 
     for (int t = 0; t < T; ++t) {
         if (t > 0) {
             const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H + (size_t)row0 * H;
-            if (!gather_rows(src, nrows, H, (unsigned)t, hl, RP, abort_flag)) s_abort = 1;
+            if (!gather_rows(src, nrows, H, (unsigned)t, hl, RP, abort_flag, p.spin_limit)) s_abort = 1;
             __syncthreads();
         }
         float ar = 0.f, az = 0.f, an = 0.f;
@@ -282,7 +284,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     bool aborted = false;
     float ddirect = 0.f;
     __shared__ int s_local;
-    const bool xlocal = group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local);
+    const bool xlocal =
+        group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local, p.spin_limit);
     __syncthreads();
 
     // global step i = T-1-t over the time range (tags and slots continue
@@ -317,7 +320,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
                 hp = (t > 1) ? y[(pbt - 1) * H + u] : h0[(size_t)b * H + u];
             }
         }
-        if (!gather_rows(slotp + (size_t)row0 * H3, nrows, H3, (unsigned)(i + 1), gl, RP, abort_flag))
+        if (!gather_rows(slotp + (size_t)row0 * H3, nrows, H3, (unsigned)(i + 1), gl, RP, abort_flag, p.spin_limit))
             s_abort = 1;
         __syncthreads();
         float acc = 0.f;
@@ -462,6 +465,7 @@ int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t st
     prm.t_end = a.t_end;
     prm.xcc_words = a.xcc_words;
     prm.xcc_tag = a.xcc_tag;
+    prm.spin_limit = a.spin_limit;
     const void* k = kernel_ptr(dir, c.pair_waves);
     if (c.lds_bytes > 65536) {
         RKA_RETURN_IF_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes));

@@ -8,6 +8,7 @@
 //   LDS-tiled         (gru_rec_tiled.hip) any hidden whose tile fits LDS.
 #include "rec_common.h"
 
+#include <atomic>
 #include <mutex>
 
 namespace rka {
@@ -18,7 +19,10 @@ struct Override {
     int kind = 0, units = 0, param = 0;
 };
 Override g_override[2];
+std::atomic<int> g_spin_limit{rec::SPIN_LIMIT};
 }  // namespace
+
+void set_rec_spin_limit(int polls) { g_spin_limit.store(polls > 0 ? polls : rec::SPIN_LIMIT); }
 
 void set_rec_override(int dir, int kind, int units, int param) {
     std::lock_guard<std::mutex> lock(g_override_mutex);
@@ -86,6 +90,7 @@ int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipSt
                       ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + slots_bytes(a.B, a.H))
                       : nullptr;
     a.xcc_tag = dir == 0 ? 1u : (unsigned)(a.T - a.t_end) + 1u;
+    a.spin_limit = g_spin_limit.load();
     if (c.kind == REC_REGISTER) return reg_launch(dir, c, a, stream);
     return tiled_launch(dir, c, a, stream);
 }

@@ -19,7 +19,9 @@ namespace rec {
 
 constexpr int NW = 8;          // wavefronts per workgroup
 constexpr int NTH = NW * 64;   // threads per workgroup
-constexpr int SPIN_LIMIT = 1 << 21;
+// Poll rounds a bounded wait makes before it gives up (default; the
+// launch passes the limit in force, see rka_set_spin_limit).
+constexpr int SPIN_LIMIT = kDefaultSpinPolls;
 constexpr int MAX_XCC_BLOCKS = 4096;  // workgroups covered by the start-up XCD check
 
 // Host-side argument bundle of one recurrence launch.
@@ -44,6 +46,7 @@ struct Args {
     // through memory); tag distinct per launch on one workspace
     unsigned long long* xcc_words = nullptr;
     unsigned xcc_tag = 0;
+    int spin_limit = SPIN_LIMIT;  // poll rounds before a wait gives up
     int B = 0, T = 0, H = 0;
     // backward: steps t_end-1 down to t_begin of a sequence of T (strides and
     // exchange tags use the global step, so consecutive ranges continue one
@@ -160,7 +163,7 @@ __device__ __forceinline__ GroupCoords group_coords(int G, int S) {
 // workspace.  Called by every thread of the workgroup (always contains a
 // barrier); words == nullptr answers false without an exchange.
 __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int first, int stride, int count,
-                                                 unsigned tag, int* abort_flag, int* s_flag) {
+                                                 unsigned tag, int* abort_flag, int* s_flag, int spin_limit) {
     if (words == nullptr) {
         __syncthreads();
         return false;
@@ -178,7 +181,7 @@ __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int 
             unsigned long long w = load_word(p);
             int spins = 0;
             while ((unsigned)(w >> 32) != tag) {
-                if (++spins > SPIN_LIMIT ||
+                if (++spins >= spin_limit ||
                     ((spins & 1023) == 0 &&
                      __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
                     __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -211,7 +214,8 @@ __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int 
 // wave of the grid would be a hot spot.
 template <int N>
 __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[N], const bool (&valid)[N],
-                                           unsigned long long (&w)[N], unsigned tag, int* abort_flag, bool& ok) {
+                                           unsigned long long (&w)[N], unsigned tag, int* abort_flag, int spin_limit,
+                                           bool& ok) {
     auto ready = [&]() {
         bool r = true;
 #pragma unroll
@@ -220,6 +224,16 @@ __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[
         for (int v = 0; v < N; ++v) r &= (!valid[v] || (unsigned)(w[v] >> 32) == tag);
         return r;
     };
+    // Giving up: a word that never came would enter the caller's sums with
+    // a stale value; NaN instead, so that whatever this step publishes from
+    // it is NaN too and no workgroup still running can turn it into a
+    // finite, wrong state.
+    auto give_up = [&]() {
+        ok = false;
+#pragma unroll
+        for (int v = 0; v < N; ++v)
+            if (valid[v] && (unsigned)(w[v] >> 32) != tag) w[v] = ((unsigned long long)tag << 32) | 0x7fc00000ull;
+    };
     if (!ok || ready()) return;
     int spins = 0;
     for (;;) {
@@ -227,13 +241,13 @@ __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[
         for (int v = 0; v < N; ++v) w[v] = load_word(p[v]);
         if (ready()) break;
         ++spins;
-        if (spins > SPIN_LIMIT) {
+        if (spins >= spin_limit) {
             __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            ok = false;
+            give_up();
             break;
         }
         if ((spins & 1023) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-            ok = false;
+            give_up();
             break;
         }
     }

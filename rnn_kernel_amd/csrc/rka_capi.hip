@@ -437,6 +437,14 @@ int rka_set_backward_chunks(int chunks) {
     return 0;
 }
 
+int rka_set_spin_limit(int polls) {
+    clear_error();
+    if (polls < 0 || polls > kDefaultSpinPolls)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "polls must be 0 (default) .. " + std::to_string(kDefaultSpinPolls));
+    set_rec_spin_limit(polls);
+    return 0;
+}
+
 int rka_backward_chunks(int seq_len) {
     clear_error();
     if (seq_len < 1) {

@@ -125,6 +125,10 @@ struct RecConfig {
 int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, RecConfig* cfg);
 // Per-direction override used by rka_set_recurrence_config: kind, units, param.
 void set_rec_override(int dir, int kind, int units, int param);
+// Poll rounds a recurrence wait makes before it gives up (0: the default,
+// which is also the largest accepted value).
+constexpr int kDefaultSpinPolls = 1 << 21;
+void set_rec_spin_limit(int polls);
 
 size_t rec_workspace_bytes(int batch, int hidden);
 int eval_gate_functions(const float* x, float* sig, float* th, int n, hipStream_t stream);

@@ -276,6 +276,71 @@ def test_recurrence_reserve_layout_matches_oracle_cache(gpu, oracle, hip_lib):
     assert _maxabs(y, f.y) <= 1e-5
 
 
+@pytest.mark.parametrize("B,T,H", [(16, 32, 256), (64, 24, 256), (6, 16, 130)])
+def test_timed_out_waits_abort_with_nan_final_states(gpu, oracle, hip_lib, rec_kind, B, T, H):
+    """Failure handling, forced from the host: with a one-poll limit
+    (rka_set_spin_limit) the recurrences' waits for other workgroups' words
+    give up, raise the launch's abort flag and end their time loops.  The
+    call still returns, the final states of aborted rows are NaN, and an
+    entry that stayed finite was computed from complete exchanges only, so
+    it equals the oracle's.  The next launch at the default limit zeroes
+    the flag with the exchange words and gives the oracle's results."""
+    from rnn_kernel_amd import _lib
+
+    p, x, h0, dy, dhn = _layer_inputs(B, T, 8, H, seed=B + T)
+    f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
+                       p["bias_ih"].numpy(), p["bias_hh"].numpy())
+    b = oracle.backward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(), f.y, f.cache,
+                        dy.numpy(), dhn.numpy())
+    gx = (x.double() @ p["weight_ih"].double().T + p["bias_ih"].double()).float().contiguous().to(gpu)
+    whh, bhh, h0d, dyd, dhnd = (t.contiguous().to(gpu) for t in (p["weight_hh"], p["bias_hh"], h0, dy, dhn))
+    y_ref = torch.as_tensor(f.y).float().to(gpu)
+    res_ref = torch.as_tensor(f.cache).float().to(gpu)
+    ws_bytes = hip_lib.rka_gru_recurrence_workspace_bytes(B, H)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def forward():
+        y = torch.empty(B, T, H, device=gpu)
+        hn = torch.empty(B, H, device=gpu)
+        rc = hip_lib.rka_gru_recurrence_forward(gx.data_ptr(), h0d.data_ptr(), whh.data_ptr(), bhh.data_ptr(),
+                                                y.data_ptr(), hn.data_ptr(), None, ws.data_ptr(), ws_bytes,
+                                                B, T, H, stream)
+        _lib.check(rc, "rka_gru_recurrence_forward")
+        torch.cuda.synchronize()
+        return hn.cpu().double()
+
+    def backward():
+        g = torch.empty(B, T, 4 * H, device=gpu)
+        dh0 = torch.empty(B, H, device=gpu)
+        rc = hip_lib.rka_gru_recurrence_backward(dyd.data_ptr(), dhnd.data_ptr(), res_ref.data_ptr(),
+                                                 h0d.data_ptr(), y_ref.data_ptr(), whh.data_ptr(), g.data_ptr(),
+                                                 dh0.data_ptr(), ws.data_ptr(), ws_bytes, B, T, H, stream)
+        _lib.check(rc, "rka_gru_recurrence_backward")
+        torch.cuda.synchronize()
+        return dh0.cpu().double()
+
+    hn_ref, dh0_ref = torch.as_tensor(f.hn), torch.as_tensor(b.dh0)
+    print(f"abort path: kind={rec_kind} B={B} T={T} H={H} fwd {_lib.describe_recurrence(0, B, H)} "
+          f"bwd {_lib.describe_recurrence(1, B, H)}", flush=True)
+    try:
+        _lib.set_spin_limit(1)
+        hn, dh0 = forward(), backward()
+    finally:
+        _lib.set_spin_limit(0)
+    for name, out, ref, tol in (("hn", hn, hn_ref, 1e-5), ("dh0", dh0, dh0_ref, GRAD_REL * float(dh0_ref.abs().max()))):
+        nan = torch.isnan(out)
+        print(f"  {name}: {int(nan.sum())} of {out.numel()} entries NaN", flush=True)
+        assert nan.any(), f"no {name} wait gave up after one poll"
+        assert not torch.isinf(out).any()
+        diff = (out - ref).abs()[~nan]
+        assert diff.numel() == 0 or float(diff.max()) <= tol
+    hn, dh0 = forward(), backward()
+    assert torch.isfinite(hn).all() and torch.isfinite(dh0).all()
+    assert float((hn - hn_ref).abs().max()) <= 1e-5
+    assert _rel(dh0, dh0_ref) <= GRAD_REL
+
+
 @pytest.mark.parametrize("B,H,local", [(64, 256, True), (8, 256, True), (4, 256, False), (3, 130, False)])
 def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H, local):
     """Each recurrence workgroup records {XCC id, launch tag} in the workspace

@@ -63,6 +63,9 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     assert hip_lib.rka_set_recurrence_config(0, 0, 0, 0) == 0
     assert hip_lib.rka_set_backward_chunks(-1) == 1001
     assert hip_lib.rka_set_backward_chunks(9) == 1001
+    assert hip_lib.rka_set_spin_limit(-1) == 1001
+    assert hip_lib.rka_set_spin_limit((1 << 21) + 1) == 1001   # above the default
+    assert hip_lib.rka_set_spin_limit(0) == 0
     assert hip_lib.rka_backward_chunks(0) == -1
 
 
