@@ -58,9 +58,19 @@ size_t rec_workspace_bytes(int batch, int hidden) { return slots_bytes(batch, hi
 
 namespace {
 
-__global__ void fill_u64_kernel(unsigned long long* __restrict__ p, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = 0ull;
+// Zeroes what a launch reads before it is written: the exchange words of
+// the slots its direction uses, the start-up XCD words of its workgroups and
+// the abort flag.
+__global__ void fill_u64_kernel(unsigned long long* __restrict__ slots, size_t n_slots,
+                                unsigned long long* __restrict__ xcc, size_t n_xcc, int* __restrict__ abort_flag) {
+    const size_t total = n_slots + n_xcc;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        if (i < n_slots)
+            slots[i] = 0ull;
+        else
+            xcc[i - n_slots] = 0ull;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) *abort_flag = 0;
 }
 
 int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipStream_t stream) {
@@ -72,23 +82,27 @@ int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipSt
     if (ws == nullptr || ws_bytes < need)
         return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "recurrence workspace too small: need " + std::to_string(need) +
                                                      " bytes, got " + std::to_string(ws_bytes));
-    // Tags start at 1, so zeroed slots never match; a fill kernel (not a
-    // memset node) keeps the sequence capturable in a HIP graph.  A range
-    // launch that continues the previous one keeps its slots (tags grow).
-    if (zero_ws) {
-        const size_t zero_words = need / sizeof(unsigned long long);
-        hipLaunchKernelGGL(fill_u64_kernel, dim3(std::min<size_t>((zero_words + 255) / 256, 1024)), dim3(256), 0,
-                           stream, reinterpret_cast<unsigned long long*>(ws), zero_words);
-        RKA_RETURN_IF_HIP(hipGetLastError());
-    }
     a.exch = reinterpret_cast<unsigned long long*>(ws);
     a.abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + need - 256);
     // Start-up XCD check words; the tag is distinct for every launch of a
     // backward sequence continued on one workspace (its first step index + 1)
     // and nonzero for a freshly zeroed one.
-    a.xcc_words = (size_t)c.groups * c.slices <= (size_t)rec::MAX_XCC_BLOCKS
+    const size_t blocks = (size_t)c.groups * c.slices;
+    a.xcc_words = blocks <= (size_t)rec::MAX_XCC_BLOCKS
                       ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + slots_bytes(a.B, a.H))
                       : nullptr;
+    // Tags start at 1, so zeroed words never match; a fill kernel (not a
+    // memset node) keeps the sequence capturable in a HIP graph.  Each slot
+    // holds [B, H] words in the forward and [B, 3H] in the backward.  A range
+    // launch that continues the previous one keeps its slots (tags grow).
+    if (zero_ws) {
+        const size_t n_slots = (size_t)2 * a.B * (dir == 0 ? 1 : 3) * a.H;
+        const size_t n_xcc = a.xcc_words ? blocks : 0;
+        const size_t n = n_slots + n_xcc;
+        hipLaunchKernelGGL(fill_u64_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
+                           stream, a.exch, n_slots, a.xcc_words, n_xcc, a.abort_flag);
+        RKA_RETURN_IF_HIP(hipGetLastError());
+    }
     a.xcc_tag = dir == 0 ? 1u : (unsigned)(a.T - a.t_end) + 1u;
     a.spin_limit = g_spin_limit.load();
     if (c.kind == REC_REGISTER) return reg_launch(dir, c, a, stream);
