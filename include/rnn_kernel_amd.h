@@ -162,15 +162,41 @@ int rka_set_backward_chunks(int chunks);
 int rka_backward_chunks(int seq_len);
 
 /* Poll rounds a recurrence kernel's wait for another workgroup's words
- * makes before it gives up (0 = the default, 2^21, also the largest value
- * accepted).  A wait that gives up raises the launch's abort flag: every
- * workgroup leaves its time loop, the aborted rows' final states (hn of the
- * forward, dh0 of the backward) are NaN, and the call itself still returns
- * 0 (the kernels are asynchronous).  Affects later launches on all threads.
- * No counterpart in the reference (its recurrence kernels step with
- * cooperative grid barriers, which wait without a bound); exported so
- * tests can drive the abort path from the host. */
+ * makes before it gives up (0 = the default, 2^24 rounds, about 2 s at the
+ * fastest poll rate; at most 2^30).  Every recurrence grid is resident, so
+ * a wait lasts about one timestep unless other kernels hold the CUs it
+ * needs.  A wait that gives up aborts the launch: every workgroup leaves its time loop and
+ * writes NaN into every output row it did not store (y and the reserve in
+ * the forward, the gate-gradient rows in the backward) and into its final
+ * states (hn, dh0), so the gradients computed from them (dW, db, dx) are
+ * NaN as well; every value an aborted launch leaves is either NaN or the
+ * value a complete run computes.  The call itself returns 0 (the kernels
+ * are asynchronous); rka_recurrence_abort_count reports the abort.
+ * Affects later launches on all threads.  No counterpart in the reference
+ * (its recurrence kernels step with cooperative grid barriers, which wait
+ * without a bound, and it refuses a grid that cannot be resident before
+ * launching, src/rnn_kernel/a100/prod/gru.py:257-263); exported so tests
+ * can drive the abort path from the host. */
 int rka_set_spin_limit(int polls);
+
+/* Failure injection for tests (-1 = off, the default): in every later
+ * recurrence launch, the workgroup with block index `block` publishes its
+ * exchange words where its partners never look for them, so their waits
+ * give up (after the rka_set_spin_limit bound) and the launch aborts, every
+ * kernel still exiting normally.  Affects later launches on all threads.
+ * No counterpart in the reference; exported so tests can force the abort
+ * path deterministically. */
+int rka_set_stall_block(int block);
+
+/* Number of recurrence calls on the current device that aborted (a wait
+ * gave up, see rka_set_spin_limit) since the library was loaded.  A call is
+ * one direction of one layer (rka_gru_forward, rka_gru_backward or a
+ * recurrence-only entry point), counted once however many of its launches
+ * (batch slices, time ranges) aborted.  Synchronises the device first, so
+ * it covers every call enqueued before.  Host code checks it at its synchronisation points; the
+ * Python front end raises RuntimeError when it has grown.  No counterpart
+ * in the reference (whose launches cannot abort). */
+int rka_recurrence_abort_count(unsigned long long* count);
 
 #define RKA_REC_AUTO 0
 #define RKA_REC_TILED 1
@@ -178,9 +204,12 @@ int rka_set_spin_limit(int polls);
 int rka_set_recurrence_config(int dir, int kind, int units, int param);
 
 /* Describe the decomposition the next recurrence call would use for this
- * shape: writes {kind, groups, slices, units, rows_per_group, pair_waves,
- * chunk, lds_bytes}. */
-int rka_describe_recurrence(int dir, int batch, int hidden_size, int out8[8]);
+ * shape: writes {kind, groups (per launch), slices, units, rows_per_group,
+ * pair_waves, chunk, lds_bytes, launches, batch_per_launch}.  A batch whose
+ * grid would not be resident on an idle GPU runs as `launches` launches
+ * over consecutive slices of batch_per_launch rows, each grid resident (the
+ * reference refuses such a batch instead, src/rnn_kernel/a100/prod/gru.py:257-263). */
+int rka_describe_recurrence(int dir, int batch, int hidden_size, int out10[10]);
 
 
 /* Evaluates the recurrence kernels' gate nonlinearities (the same device

@@ -4,10 +4,13 @@ from .gru import (
     GRU,
     GRUFunction,
     MAX_HIDDEN_SIZE,
+    RecurrenceAbortedError,
+    check_recurrences,
     from_torch_gru,
     gru_forward_inference,
     is_available,
     is_supported_gru,
+    set_strict,
 )
 from .train import AdamW, HeadFunction, LinearHead, MSELossFunction, mse_loss
 
@@ -20,8 +23,11 @@ __all__ = [
     "GRU",
     "GRUFunction",
     "MAX_HIDDEN_SIZE",
+    "RecurrenceAbortedError",
+    "check_recurrences",
     "from_torch_gru",
     "gru_forward_inference",
     "is_available",
     "is_supported_gru",
+    "set_strict",
 ]

@@ -35,6 +35,8 @@ SIGNATURES = {
     "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
     "rka_set_backward_chunks": (_I, [_I]),
     "rka_set_spin_limit": (_I, [_I]),
+    "rka_recurrence_abort_count": (_I, [ctypes.POINTER(ctypes.c_ulonglong)]),
+    "rka_set_stall_block": (_I, [_I]),
     "rka_backward_chunks": (_I, [_I]),
     "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
     "rka_eval_gate_functions": (_I, [_P, _P, _P, _I, _P]),
@@ -117,9 +119,10 @@ REC_KINDS = {0: "auto", 1: "tiled", 2: "register"}
 
 def describe_recurrence(direction: int, batch: int, hidden: int) -> dict:
     """Decomposition the next recurrence call would use (0 forward, 1 backward)."""
-    out = (ctypes.c_int * 8)()
+    out = (ctypes.c_int * 10)()
     check(load().rka_describe_recurrence(direction, batch, hidden, out), "rka_describe_recurrence")
-    keys = ("kind", "groups", "slices", "units", "rows", "pair_waves", "chunk", "lds_bytes")
+    keys = ("kind", "groups", "slices", "units", "rows", "pair_waves", "chunk", "lds_bytes", "launches",
+            "batch_per_launch")
     d = dict(zip(keys, list(out)))
     d["kind"] = REC_KINDS.get(d["kind"], d["kind"])
     return d
@@ -135,9 +138,22 @@ def set_backward_chunks(chunks: int) -> None:
 
 
 def set_spin_limit(polls: int) -> None:
-    """Poll rounds a recurrence wait makes before it gives up (0 = default);
-    see rka_set_spin_limit."""
+    """Poll rounds a recurrence wait makes before it gives up (0 = the
+    default, 2^24); see rka_set_spin_limit."""
     check(load().rka_set_spin_limit(polls), "rka_set_spin_limit")
+
+
+def set_stall_block(block: int) -> None:
+    """Failure injection for tests (-1 = off); see rka_set_stall_block."""
+    check(load().rka_set_stall_block(block), "rka_set_stall_block")
+
+
+def recurrence_abort_count() -> int:
+    """Aborted recurrence calls on the current device so far (synchronises
+    the device); see rka_recurrence_abort_count."""
+    n = ctypes.c_ulonglong(0)
+    check(load().rka_recurrence_abort_count(ctypes.byref(n)), "rka_recurrence_abort_count")
+    return int(n.value)
 
 
 def backward_chunks(seq_len: int) -> int:

@@ -60,7 +60,9 @@ struct RegParams {
     int t_begin, t_end;  // backward: time range processed
     unsigned long long* xcc_words;  // start-up XCD check (nullable)
     unsigned xcc_tag;
-    int spin_limit;  // poll rounds before a wait gives up
+    int spin_limit;                       // poll rounds before a wait gives up
+    unsigned long long* abort_count;      // per-device count of aborted launches
+    int stall_block;                      // test failure injection (rec::Args::stall_block)
 };
 
 // Forward recurrence, S = ceil(H / 64) slices of 64 units (one workgroup
@@ -173,9 +175,9 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         load_gx(gxs[0], 0);
     }
     if (threadIdx.x == 0) s_abort = 0;
+    const rec::WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
     __shared__ int s_local;
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local,
-                                                   p.spin_limit);
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
 
     // Lane l < 2 NP polls half l / NP, slot 1 + (l % NP) / 8, entry l % 8 of
     // every row; other lanes, and lanes of a k past H, re-read the wave's
@@ -199,6 +201,11 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         roff[r] = (rvalid[r] ? row0 + r : row0) * H;
     }
 
+    // the owner lane's word in the slot of each step parity, as 32-bit
+    // offsets (2 B H < 2^31); the failure injection swaps the two
+    const int pub_flip = (int)blockIdx.x == p.stall_block ? 1 : 0;
+    const unsigned pub_off[2] = {(unsigned)(pub_flip * B * H + orow * H + u),
+                                 (unsigned)((1 - pub_flip) * B * H + orow * H + u)};
     // outputs of the previous step, stored after the next poll
     float o_h = 0.f, o_r = 0.f, o_z = 0.f, o_n = 0.f, o_a = 0.f;
     float* y_row = y + (size_t)orow * T * H + u;
@@ -213,16 +220,30 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
             cp[3 * H] = o_a;
         }
     };
-    // partial sums of the step in flight per row; the own slot's FMAs land first
-    float ar[R][2], az[R][2], an[R][2];
+    // partial sums of the step in flight per row; the own slot's FMAs land
+    // first.  Two accumulators per gate and row give each wave six
+    // independent FMA chains; with four rows there are twelve chains with
+    // one, which keeps that variant within 256 VGPRs (no scratch).
+    constexpr int NACC = R == 4 ? 1 : 2;
+    float ar[R][NACC], az[R][NACC], an[R][NACC];
     // slot j's FMAs of row r with its eight h values (wave-uniform)
     auto fma8 = [&](const float (&hv)[8], int j, int r) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            ar[r][i & 1] = fmaf(hv[i], wr[8 * j + i], ar[r][i & 1]);
-            az[r][i & 1] = fmaf(hv[i], wz[8 * j + i], az[r][i & 1]);
-            an[r][i & 1] = fmaf(hv[i], wn[8 * j + i], an[r][i & 1]);
+            ar[r][i % NACC] = fmaf(hv[i], wr[8 * j + i], ar[r][i % NACC]);
+            az[r][i % NACC] = fmaf(hv[i], wz[8 * j + i], az[r][i % NACC]);
+            an[r][i % NACC] = fmaf(hv[i], wn[8 * j + i], an[r][i % NACC]);
         }
+    };
+    auto zero_acc = [&](int r) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a) ar[r][a] = az[r][a] = an[r][a] = 0.f;
+    };
+    auto acc_sum = [](const float (&a)[NACC]) {
+        if constexpr (NACC == 2)
+            return a[0] + a[1];
+        else
+            return a[0];
     };
     // eight consecutive floats of LDS as wave-uniform values
     auto lds8 = [](const float* src, float (&hv)[8]) {
@@ -234,7 +255,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     auto local_fmas = [&](int par) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            ar[r][0] = ar[r][1] = az[r][0] = az[r][1] = an[r][0] = an[r][1] = 0.f;
+            zero_acc(r);
             float hl[8];
             lds8(&hloc[par][r][16 * Q + 8 * hf], hl);
             fma8(hl, 0, r);
@@ -246,7 +267,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     // step 0's own slot from h0
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        ar[r][0] = ar[r][1] = az[r][0] = az[r][1] = an[r][0] = an[r][1] = 0.f;
+        zero_acc(r);
         float hv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -272,7 +293,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
                     pv[r] = pvalid && rvalid[r];
                 }
                 bool ok = true;
-                rec::wait_words<R>(pp, pv, first_read, (unsigned)t, abort_flag, p.spin_limit, ok);
+                rec::wait_words<R>(pp, pv, first_read, (unsigned)t, wc, ok);
 #pragma unroll
                 for (int r = 0; r < R; ++r) hx[r] = pv[r] ? __uint_as_float((unsigned)first_read[r]) : 0.f;
                 if (!ok) s_abort = 1;
@@ -299,15 +320,20 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         }
         // @probe:polled
         if constexpr (NR > 0) {
-            if constexpr (R > 1) {
+            // four rows at four slices: every row one slot's h values at a
+            // time (registers); otherwise row 0 all slots at once
+            constexpr bool by_slot = R == 4 && S == 4;
+            if constexpr (R > 1 && !by_slot) {
 #pragma unroll
                 for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][8 * jj], hv0[jj]);
             }
+            if constexpr (!by_slot) {
 #pragma unroll
-            for (int jj = 0; jj < NR; ++jj) fma8(hv0[jj], jj + 1, 0);
+                for (int jj = 0; jj < NR; ++jj) fma8(hv0[jj], jj + 1, 0);
+            }
 #pragma unroll
-            for (int r = 1; r < R; ++r) {
-                if constexpr (R == 4 && S == 4) {
+            for (int r = by_slot ? 0 : 1; r < R; ++r) {
+                if constexpr (by_slot) {
                     // one slot's h values at a time (registers)
 #pragma unroll
                     for (int jj = 0; jj < NR; ++jj) {
@@ -331,7 +357,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         for (int r = 0; r < R; ++r) {
             // halves: lanes 0-31 get the r sum and lanes 32-63 the z sum of
             // unit fu, every lane the n sum (lower half + upper half)
-            const float r0 = ar[r][0] + ar[r][1], z0 = az[r][0] + az[r][1], n0 = an[r][0] + an[r][1];
+            const float r0 = acc_sum(ar[r]), z0 = acc_sum(az[r]), n0 = acc_sum(an[r]);
             const auto prz = __builtin_amdgcn_permlane32_swap(__float_as_uint(r0), __float_as_uint(z0), false, false);
             const auto pn = __builtin_amdgcn_permlane32_swap(__float_as_uint(n0), __float_as_uint(n0), false, false);
             part[t & 1][Q][hf][r][fu] = __uint_as_float(prz[0]) + __uint_as_float(prz[1]);
@@ -354,9 +380,15 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
             const float z = rec::sigmoid_f(cur[1] + sz);
             const float n = rec::tanh_f(cur[2] + r * sn);
             const float h = n + z * (h_prev - n);
-            if constexpr (NR > 0)
-                rec::publish_word(exch + (size_t)(t & 1) * B * H + (size_t)orow * H + u,
-                                  rec::pack_word(h, (unsigned)(t + 1)), xlocal);
+            if constexpr (NR > 0) {
+                // the offset made opaque here, so the 64-bit address is
+                // formed per step instead of one per step parity being kept
+                // across the loop (at four rows and four slices that pair no
+                // longer fits the 256 VGPRs)
+                unsigned off = pub_off[t & 1];
+                asm volatile("" : "+v"(off));
+                rec::publish_word(exch + off, rec::pack_word(h, (unsigned)(t + 1)), xlocal);
+            }
             o_h = h;
             o_r = r;
             o_z = z;
@@ -380,20 +412,28 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         // @probe:step_end
         return !abort_now;
     };
-    bool aborted = false;
+    // step t stores the outputs of step t - 1: after a step that aborts,
+    // rows t_stop .. T-1 were not stored
+    int t_stop = T;
     for (int t = 0; t < T; t += 2) {
         if (!step(t, gxs[0], gxs[1])) {
-            aborted = true;
+            t_stop = t;
             break;
         }
         if (t + 1 < T && !step(t + 1, gxs[1], gxs[0])) {
-            aborted = true;
+            t_stop = t + 1;
             break;
         }
     }
     // @probe:kernel_end
+    const bool aborted = t_stop < T;
     if (owner) {
-        if (!aborted) store_outputs(T - 1);
+        if (!aborted) {
+            store_outputs(T - 1);
+        } else {
+            o_h = o_r = o_z = o_n = o_a = __builtin_nanf("");
+            for (int t = t_stop; t < T; ++t) store_outputs(t);
+        }
         hn[(size_t)orow * H + u] = aborted ? __builtin_nanf("") : h_prev;
     }
 }
@@ -508,6 +548,11 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
 
     // wave r < R owns row row0 + r: its pointwise math, G stores and words
     const int orow = row0 + (wave < R ? wave : 0);
+    // the owner lane's first word in the slot of each step parity (32-bit
+    // offsets, 6 B H < 2^31); the failure injection swaps the two
+    const int pub_flip = (int)blockIdx.x == p.stall_block ? 1 : 0;
+    const unsigned pub_off[2] = {(unsigned)(pub_flip * B * H3 + orow * H3 + u),
+                                 (unsigned)((1 - pub_flip) * B * H3 + orow * H3 + u)};
     const bool owner = wave < R && uvalid && orow < B;
     float dh = 0.f, ddirect = 0.f;
     float o_dan = 0.f, o_drh = 0.f, o_dzh = 0.f, o_dnh = 0.f;
@@ -534,9 +579,9 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         if (i0 + 1 < i1) load_inputs(ins[1], T - 2 - i0);
     }
     if (threadIdx.x == 0) s_abort = 0;
+    const rec::WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
     __shared__ int s_local;
-    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local,
-                                                   p.spin_limit);
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
 
     // Wave w polls remote entries WE w .. WE w + WE - 1 of every row:
     // register 0 lane l entry WE w + l (l < WE), register 1 (S = 4: WE = 72)
@@ -581,7 +626,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
             ddirect = gsum * cz;
             if constexpr (RE > 0) {
                 const unsigned tag = (unsigned)(i + 1);
-                unsigned long long* wp = exch + (size_t)(i & 1) * B * H3 + (size_t)orow * H3 + u;
+                unsigned long long* wp = exch + pub_off[i & 1];
                 unsigned long long* const pp3[3] = {wp, wp + H, wp + 2 * H};
                 const unsigned long long w3[3] = {rec::pack_word(o_drh, tag), rec::pack_word(o_dzh, tag),
                                                   rec::pack_word(o_dan, tag)};
@@ -659,7 +704,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
                 }
             }
             bool ok = true;
-            rec::wait_words<NW2 * R>(pp, pv, first_read, (unsigned)(i + 1), abort_flag, p.spin_limit, ok);
+            rec::wait_words<NW2 * R>(pp, pv, first_read, (unsigned)(i + 1), wc, ok);
             if (!ok) s_abort = 1;
             // polled entry e of the wave to row e / RE, position e % RE of its
             // LDS block (one wave writes and reads the blocks; LDS keeps a
@@ -725,19 +770,34 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     __syncthreads();
     first_poll(i0);
     local_fmas();
-    bool aborted = false;
+    // step i stores the G row of step i: after a step that aborts, rows
+    // i_stop + 1 .. i1 - 1 were not stored
+    int i_stop = i1;
     for (int i = i0; i < i1; i += 2) {
         if (!step(i, ins[0], ins[1])) {
-            aborted = true;
+            i_stop = i;
             break;
         }
         if (i + 1 < i1 && !step(i + 1, ins[1], ins[0])) {
-            aborted = true;
+            i_stop = i + 1;
             break;
         }
     }
     // @probe:kernel_end
-    if (owner) dh0[(size_t)orow * H + u] = aborted ? __builtin_nanf("") : dh;
+    const bool aborted = i_stop < i1;
+    if (owner) {
+        if (aborted) {
+            const float nan = __builtin_nanf("");
+            for (int i = i_stop + 1; i < i1; ++i) {
+                float* op = gout + ((size_t)orow * T + (T - 1 - i)) * 4 * H;
+                op[u] = nan;
+                op[H + u] = nan;
+                op[2 * H + u] = nan;
+                op[3 * H + u] = nan;
+            }
+        }
+        dh0[(size_t)orow * H + u] = aborted ? __builtin_nanf("") : dh;
+    }
 }
 
 // ------------------------------------------------------------- config ---
@@ -777,10 +837,7 @@ void chunk_of(int dir, int H, int* chunk, int* cap) {
 
 }  // namespace
 
-// Batch rows per workgroup the local-slice kernels are built for.  (The
-// forward with four rows at four slices keeps two addresses in scratch; it
-// still beats two rows run in two waves of workgroups: 2.30 vs 3.08 ms per
-// c4 layer.)
+// Batch rows per workgroup the local-slice kernels are built for.
 int max_rows(int dir, int slices) {
     (void)dir;
     (void)slices;
@@ -788,9 +845,8 @@ int max_rows(int dir, int slices) {
 }
 
 // The fewest rows per workgroup whose B·S workgroups are resident; when
-// none is, the most rows (then the grid runs in waves of resident groups:
-// a group's workgroups are consecutive in its XCD's in-order dispatch, so
-// every dispatched group can finish and free its CUs for the next).
+// none is, the most rows, and the batch runs as several launches over
+// slices whose grids are resident.
 int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_units, int fixed_rows,
                RecConfig* cfg) {
     int chunk = 0, cap = 0;
@@ -804,20 +860,25 @@ int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_
                                                    std::to_string(max_rows(dir, S)) + " rows at hidden_size " +
                                                    std::to_string(hidden));
     int chosen = 0;
+    long chosen_cap = 0;
     for (int rows : {1, 2, 4}) {
         if (rows > max_rows(dir, S) || (fixed_rows && rows != fixed_rows)) continue;
         const int G = (batch + rows - 1) / rows;
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows, S), NTH, 0) != hipSuccess)
             continue;
-        if ((long)G * S <= (long)per_cu * dev.num_cus) {
-            chosen = rows;
-            break;
-        }
+        const long resident = (long)per_cu * dev.num_cus;
+        chosen = rows;  // the last candidate (the most rows) unless one fits
+        chosen_cap = resident;
+        if ((long)G * S <= resident) break;
     }
-    if (chosen == 0) chosen = fixed_rows ? fixed_rows : max_rows(dir, S);
+    if (chosen == 0 || chosen_cap < S)
+        return fail(RKA_ERR_TOO_LARGE_FOR_RESIDENT_LAUNCH, "register-resident recurrence: no resident grid at hidden_size " +
+                                                               std::to_string(hidden));
     cfg->kind = REC_REGISTER;
-    cfg->groups = (batch + chosen - 1) / chosen;
+    cfg->batch_per_launch = batch_per_resident_launch(batch, chosen, S, chosen_cap);
+    cfg->launches = (batch + cfg->batch_per_launch - 1) / cfg->batch_per_launch;
+    cfg->groups = (cfg->batch_per_launch + chosen - 1) / chosen;
     cfg->slices = S;
     cfg->units = 64;
     cfg->rows = chosen;
@@ -834,7 +895,7 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     const bool aligned = (reinterpret_cast<uintptr_t>(a.w_hh) & 15u) == 0;
     RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
                   (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end,
-                  a.xcc_words, a.xcc_tag, a.spin_limit};
+                  a.xcc_words, a.xcc_tag, a.spin_limit, a.abort_count, a.stall_block};
     const void* k = kernel_ptr(dir, cap, c.rows, c.slices);
     if (k == nullptr) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: no kernel for this row count");
     if (dir == 0) {

@@ -35,14 +35,16 @@ struct RecParams {
     int t_begin, t_end;  // backward: time range processed
     unsigned long long* xcc_words;  // start-up XCD check (nullable)
     unsigned xcc_tag;
-    int spin_limit;  // poll rounds before a wait gives up
+    int spin_limit;                       // poll rounds before a wait gives up
+    unsigned long long* abort_count;      // per-device count of aborted launches
+    int stall_block;                      // test failure injection (rec::Args::stall_block)
 };
 
 // Gathers `nrows` rows of `len` published words with step tag `tag` from
 // src (row stride `len`) into LDS rows of stride RP.  Returns false when the
-// spin budget ran out or another workgroup raised the abort flag.
+// wait gave up (see rec::WaitCtl) or another workgroup raised the abort flag.
 __device__ bool gather_rows(const unsigned long long* __restrict__ src, int nrows, int len, unsigned tag,
-                            float* __restrict__ dst, int RP, int* __restrict__ abort_flag, int spin_limit) {
+                            float* __restrict__ dst, int RP, const rec::WaitCtl& wc) {
     using namespace rec;
     const int total = nrows * len;
     bool ok = true;
@@ -60,13 +62,12 @@ __device__ bool gather_rows(const unsigned long long* __restrict__ src, int nrow
             int spins = 0;
             while ((unsigned)(w[j] >> 32) != tag) {
                 if (!ok) break;
-                if (++spins >= spin_limit) {
-                    __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (++spins >= wc.spin_limit) {
+                    raise_abort(wc);
                     ok = false;
                     break;
                 }
-                if ((spins & 1023) == 0 &&
-                    __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                if ((spins & 1023) == 0 && abort_raised(wc)) {
                     ok = false;
                     break;
                 }
@@ -148,17 +149,20 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
     const int kend = min(p.KLEN, kbeg + p.KCH);
     const float* wr = Wl + (ul * 3) * RP;
     const float* hrow = hl + bl * RP;
-    bool aborted = false;
+    // iteration t stores the outputs of step t: after an iteration that
+    // aborts, rows t_stop .. T-1 were not stored
+    int t_stop = T;
+    const int pub_flip = (int)blockIdx.x == p.stall_block ? 1 : 0;  // test failure injection
+    const WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
     __shared__ int s_local;
     // the group = the S workgroups of rec::group_coords; plain publishing stores when they share an XCD
-    const bool xlocal =
-        group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local, p.spin_limit);
+    const bool xlocal = group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
     __syncthreads();
 
     for (int t = 0; t < T; ++t) {
         if (t > 0) {
             const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H + (size_t)row0 * H;
-            if (!gather_rows(src, nrows, H, (unsigned)t, hl, RP, abort_flag, p.spin_limit)) s_abort = 1;
+            if (!gather_rows(src, nrows, H, (unsigned)t, hl, RP, wc)) s_abort = 1;
             __syncthreads();
         }
         float ar = 0.f, az = 0.f, an = 0.f;
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
         pp[2 * NP + pair] = an;
         __syncthreads();
         if (s_abort) {
-            aborted = true;
+            t_stop = t;
             break;
         }
         if (owner) {
@@ -198,7 +202,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
             const float z = sigmoid_f(gxz + sz);
             const float n = tanh_f(gxn + r * sn);
             const float h = n + z * (h_prev - n);
-            publish_word(exch + (size_t)(t & 1) * B * H + (size_t)b * H + u, pack_word(h, (unsigned)(t + 1)), xlocal);
+            publish_word(exch + (size_t)((t & 1) ^ pub_flip) * B * H + (size_t)b * H + u,
+                         pack_word(h, (unsigned)(t + 1)), xlocal);
             const size_t bt = (size_t)b * T + t;
             y[bt * H + u] = h;
             if (reserve) {
@@ -217,7 +222,22 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
             }
         }
     }
-    if (owner) hn[(size_t)b * H + u] = aborted ? __builtin_nanf("") : h_prev;
+    const bool aborted = t_stop < T;
+    if (owner) {
+        const float nan = __builtin_nanf("");
+        for (int t = t_stop; t < T; ++t) {
+            const size_t bt = (size_t)b * T + t;
+            y[bt * H + u] = nan;
+            if (reserve) {
+                float* cp = reserve + bt * 4 * H;
+                cp[u] = nan;
+                cp[H + u] = nan;
+                cp[2 * H + u] = nan;
+                cp[3 * H + u] = nan;
+            }
+        }
+        hn[(size_t)b * H + u] = aborted ? nan : h_prev;
+    }
 }
 
 // ------------------------------------------------------------ backward ---
@@ -281,16 +301,20 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     const int kend = min(p.KLEN, kbeg + p.KCH);
     const float* wrow = Wt + ul * RP;
     const float* grow = gl + bl * RP;
-    bool aborted = false;
+    // iteration i stores the G row of step i: after an iteration that
+    // aborts, rows i_stop + 1 .. T - 1 - t_begin were not stored
+    const int i1 = T - p.t_begin;
+    int i_stop = i1;
+    const int pub_flip = (int)blockIdx.x == p.stall_block ? 1 : 0;  // test failure injection
     float ddirect = 0.f;
+    const WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
     __shared__ int s_local;
-    const bool xlocal =
-        group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, abort_flag, &s_local, p.spin_limit);
+    const bool xlocal = group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
     __syncthreads();
 
     // global step i = T-1-t over the time range (tags and slots continue
     // across consecutive range launches)
-    for (int i = T - p.t_end; i < T - p.t_begin; ++i) {
+    for (int i = T - p.t_end; i < i1; ++i) {
         const int t = T - 1 - i;
         unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
         if (owner) {
@@ -302,7 +326,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
             const float dzh = dz * cz * (1.0f - cz);
             ddirect = gsum * cz;
             const unsigned tag = (unsigned)(i + 1);
-            unsigned long long* wp = slotp + (size_t)b * H3 + u;
+            unsigned long long* wp = exch + (size_t)((i & 1) ^ pub_flip) * B * H3 + (size_t)b * H3 + u;
             publish_word(wp, pack_word(drh, tag), xlocal);
             publish_word(wp + H, pack_word(dzh, tag), xlocal);
             publish_word(wp + 2 * H, pack_word(dan, tag), xlocal);
@@ -320,8 +344,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
                 hp = (t > 1) ? y[(pbt - 1) * H + u] : h0[(size_t)b * H + u];
             }
         }
-        if (!gather_rows(slotp + (size_t)row0 * H3, nrows, H3, (unsigned)(i + 1), gl, RP, abort_flag, p.spin_limit))
-            s_abort = 1;
+        if (!gather_rows(slotp + (size_t)row0 * H3, nrows, H3, (unsigned)(i + 1), gl, RP, wc)) s_abort = 1;
         __syncthreads();
         float acc = 0.f;
         if (slot) {
@@ -335,7 +358,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
         part[((i & 1) * KC + kc) * NP + pair] = acc;
         __syncthreads();
         if (s_abort) {
-            aborted = true;
+            i_stop = i;
             break;
         }
         if (owner) {
@@ -346,7 +369,18 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
             dh = sum;
         }
     }
-    if (owner) dh0[(size_t)b * H + u] = aborted ? __builtin_nanf("") : dh;
+    const bool aborted = i_stop < i1;
+    if (owner) {
+        const float nan = __builtin_nanf("");
+        for (int i = i_stop + 1; i < i1; ++i) {
+            float* op = gout + ((size_t)b * T + (T - 1 - i)) * 4 * H;
+            op[u] = nan;
+            op[H + u] = nan;
+            op[2 * H + u] = nan;
+            op[3 * H + u] = nan;
+        }
+        dh0[(size_t)b * H + u] = aborted ? nan : dh;
+    }
 }
 
 int rows_padded(int len) {
@@ -408,6 +442,10 @@ RecParams make_params(int dir, int B, int T, int H, const RecConfig& c) {
 
 }  // namespace
 
+// The decomposition with the lowest modelled cost among those whose tile
+// fits LDS.  A grid that is not resident for the whole batch runs as
+// launches over batch slices of the most groups that are (the cost of a
+// step then counts once per launch).
 int tiled_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_u, int fixed_pw, RecConfig* cfg) {
     const int ncu = dev.num_cus > 0 ? dev.num_cus : 256;
     const int lds_cap = dev.max_lds_per_block > 0 ? dev.max_lds_per_block : 65536;
@@ -422,20 +460,22 @@ int tiled_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixe
             if (Bg < 1) continue;
             // Only use PW > 1 when its extra rows are needed.
             if (PW > 1 && (PW / 2) * (64 / U) >= batch && !fixed_pw) continue;
-            const int G = (batch + Bg - 1) / Bg;
             const int S = (hidden + U - 1) / U;
             const int lds = lds_bytes_for(dir, hidden, U, Bg, PW);
             if (lds > lds_cap) continue;
-            const int nwg = G * S;
             const int cap = max_resident(dev, dir, PW, lds);
-            if (nwg > cap) continue;
+            if (cap < S) continue;
+            const int per_launch = batch_per_resident_launch(batch, Bg, S, cap);
+            const int launches = (batch + per_launch - 1) / per_launch;
+            const int G = (per_launch + Bg - 1) / Bg;
+            const int nwg = G * S;
             // Per-step cost model fitted to measured sweeps: the number of
             // slices exchanging per group dominates, then per-workgroup work
             // (times the workgroups sharing a CU) and the gathered volume.
             const double work = (double)Bg * U * hidden * 3.0 / (64.0 * PW);
             const double share = std::ceil((double)nwg / ncu);
             const double xfer = (double)Bg * hidden * (dir == 0 ? 1 : 3) / rec::NTH;
-            double score = work * share + 4.0 * xfer + 60.0 * S;
+            double score = (work * share + 4.0 * xfer + 60.0 * S) * launches;
             if (!found || score < best) {
                 found = true;
                 best = score;
@@ -447,13 +487,15 @@ int tiled_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixe
                 best_cfg.pair_waves = PW;
                 best_cfg.chunk = 0;
                 best_cfg.lds_bytes = lds;
+                best_cfg.launches = launches;
+                best_cfg.batch_per_launch = per_launch;
             }
         }
     }
     if (!found) {
         return fail(RKA_ERR_TOO_LARGE_FOR_RESIDENT_LAUNCH,
-                    "no resident decomposition of the " + std::string(dir == 0 ? "forward" : "backward") +
-                        " recurrence fits: batch=" + std::to_string(batch) + ", hidden=" + std::to_string(hidden));
+                    "no decomposition of the " + std::string(dir == 0 ? "forward" : "backward") +
+                        " recurrence fits LDS: hidden=" + std::to_string(hidden));
     }
     *cfg = best_cfg;
     return 0;
@@ -466,6 +508,8 @@ int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t st
     prm.xcc_words = a.xcc_words;
     prm.xcc_tag = a.xcc_tag;
     prm.spin_limit = a.spin_limit;
+    prm.abort_count = a.abort_count;
+    prm.stall_block = a.stall_block;
     const void* k = kernel_ptr(dir, c.pair_waves);
     if (c.lds_bytes > 65536) {
         RKA_RETURN_IF_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes));

@@ -1,15 +1,23 @@
 // Recurrence dispatcher: picks the kernel family and decomposition for a
-// shape, zeroes the exchange slots and launches one persistent kernel.
+// shape, zeroes the exchange slots and launches the persistent kernel once
+// per batch slice.
 //
-// Families (both persistent, one launch per layer and direction, the time
-// loop inside the kernel; a plain launch, the block-to-group mapping of
-// rec::group_coords guaranteeing progress without co-residency):
+// Families (both persistent, the time loop inside the kernel, a plain
+// launch of a grid that is resident on an idle GPU; a batch whose grid is
+// not resident runs as several launches over batch slices):
 //   register-resident (gru_rec_reg.hip)  hidden <= 256, W_hh slice in VGPRs;
 //   LDS-tiled         (gru_rec_tiled.hip) any hidden whose tile fits LDS.
 #include "rec_common.h"
 
 #include <atomic>
 #include <mutex>
+#include <vector>
+
+// Count of recurrence calls that aborted (a wait gave up), one per device;
+// raised by the kernels through the pointer passed in their arguments, read
+// by rka_recurrence_abort_count.  The abort flag is zeroed once per call
+// (with the exchange words), so a call counts once.
+__device__ unsigned long long rka_rec_abort_count;
 
 namespace rka {
 
@@ -19,10 +27,47 @@ struct Override {
     int kind = 0, units = 0, param = 0;
 };
 Override g_override[2];
-std::atomic<int> g_spin_limit{rec::SPIN_LIMIT};
+std::atomic<int> g_spin_limit{kDefaultSpinPolls};
+std::atomic<int> g_stall_block{-1};
+
+std::mutex g_count_mutex;
+std::vector<unsigned long long*> g_count_ptr;  // per device: address of rka_rec_abort_count
+
+// Device address of this device's abort counter (the variable's host-side
+// name is not a device address).
+int abort_counter(int dev, unsigned long long** out) {
+    std::lock_guard<std::mutex> lock(g_count_mutex);
+    if ((int)g_count_ptr.size() <= dev) g_count_ptr.resize(dev + 1, nullptr);
+    if (!g_count_ptr[dev]) {
+        void* p = nullptr;
+        RKA_RETURN_IF_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(rka_rec_abort_count)));
+        g_count_ptr[dev] = reinterpret_cast<unsigned long long*>(p);
+    }
+    *out = g_count_ptr[dev];
+    return 0;
+}
 }  // namespace
 
-void set_rec_spin_limit(int polls) { g_spin_limit.store(polls > 0 ? polls : rec::SPIN_LIMIT); }
+void set_rec_spin_limit(int polls) { g_spin_limit.store(polls > 0 ? polls : kDefaultSpinPolls); }
+void set_rec_stall_block(int block) { g_stall_block.store(block); }
+
+int rec_abort_count(unsigned long long* count) {
+    const DeviceInfo* dev = nullptr;
+    RKA_RETURN_IF_ERR(current_device_info(&dev));
+    unsigned long long* p = nullptr;
+    RKA_RETURN_IF_ERR(abort_counter(dev->device, &p));
+    RKA_RETURN_IF_HIP(hipDeviceSynchronize());
+    RKA_RETURN_IF_HIP(hipMemcpy(count, p, sizeof(unsigned long long), hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int batch_per_resident_launch(int batch, int rows, int S, long cap) {
+    const long G = (batch + rows - 1) / rows;
+    if (G * S <= cap) return batch;
+    long groups = cap / S;
+    if (groups >= 8) groups -= groups % 8;
+    return (int)std::min<long>(batch, groups * rows);
+}
 
 void set_rec_override(int dir, int kind, int units, int param) {
     std::lock_guard<std::mutex> lock(g_override_mutex);
@@ -73,6 +118,47 @@ __global__ void fill_u64_kernel(unsigned long long* __restrict__ slots, size_t n
     if (blockIdx.x == 0 && threadIdx.x == 0) *abort_flag = 0;
 }
 
+// Launches the recurrence of direction `dir` over the whole batch: one
+// launch per batch slice of c.batch_per_launch rows (pointers offset to the
+// slice's rows).  Slice k uses its own part of the exchange slots (words
+// [2 r0 W, 2 (r0 + rows) W) for its first row r0, W = H forward, 3H
+// backward) and start-up XCD words tagged with k, so consecutive time ranges
+// of a chunked backward continue each slice on the same, once-zeroed
+// workspace: tags are (steps done before this range) * launches + k + 1.
+int launch_slices(int dir, const RecConfig& c, rec::Args a, unsigned long long* xcc_base, hipStream_t stream) {
+    const int B = a.B, T = a.T, H = a.H;
+    const size_t W = (size_t)(dir == 0 ? 1 : 3) * H;
+    const unsigned long long* exch0 = a.exch;
+    for (int k = 0; k < c.launches; ++k) {
+        const int r0 = k * c.batch_per_launch;
+        const int Bs = std::min(c.batch_per_launch, B - r0);
+        RecConfig cs = c;
+        cs.groups = (Bs + c.rows - 1) / c.rows;
+        rec::Args s = a;
+        s.B = Bs;
+        auto off = [&](auto* p, size_t per_row) { return p ? p + (size_t)r0 * per_row : p; };
+        s.gx = off(a.gx, (size_t)T * 3 * H);
+        s.dy = off(a.dy, (size_t)T * H);
+        s.dhn = off(a.dhn, (size_t)H);
+        s.hn = off(a.hn, (size_t)H);
+        s.gout = off(a.gout, (size_t)T * 4 * H);
+        s.dh0 = off(a.dh0, (size_t)H);
+        s.h0 = off(a.h0, (size_t)H);
+        s.y = off(a.y, (size_t)T * H);
+        s.reserve = off(a.reserve, (size_t)T * 4 * H);
+        s.exch = const_cast<unsigned long long*>(exch0) + 2 * (size_t)r0 * W;
+        const size_t blocks = (size_t)cs.groups * cs.slices;
+        s.xcc_words = blocks <= (size_t)rec::MAX_XCC_BLOCKS ? xcc_base : nullptr;
+        s.xcc_tag = (unsigned)((size_t)(T - a.t_end) * c.launches + k + 1);
+        if (cs.kind == REC_REGISTER) {
+            RKA_RETURN_IF_ERR(reg_launch(dir, cs, s, stream));
+        } else {
+            RKA_RETURN_IF_ERR(tiled_launch(dir, cs, s, stream));
+        }
+    }
+    return 0;
+}
+
 int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipStream_t stream) {
     const DeviceInfo* dev = nullptr;
     RKA_RETURN_IF_ERR(current_device_info(&dev));
@@ -82,31 +168,28 @@ int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipSt
     if (ws == nullptr || ws_bytes < need)
         return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "recurrence workspace too small: need " + std::to_string(need) +
                                                      " bytes, got " + std::to_string(ws_bytes));
+    if ((size_t)a.T * c.launches + c.launches >= 0xffffffffull)
+        return fail(RKA_ERR_UNSUPPORTED_SHAPE, "recurrence: seq_len times batch slices exceeds the 32-bit step tags");
     a.exch = reinterpret_cast<unsigned long long*>(ws);
     a.abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + need - 256);
-    // Start-up XCD check words; the tag is distinct for every launch of a
-    // backward sequence continued on one workspace (its first step index + 1)
-    // and nonzero for a freshly zeroed one.
-    const size_t blocks = (size_t)c.groups * c.slices;
-    a.xcc_words = blocks <= (size_t)rec::MAX_XCC_BLOCKS
-                      ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + slots_bytes(a.B, a.H))
-                      : nullptr;
+    RKA_RETURN_IF_ERR(abort_counter(dev->device, &a.abort_count));
+    unsigned long long* xcc = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + slots_bytes(a.B, a.H));
     // Tags start at 1, so zeroed words never match; a fill kernel (not a
     // memset node) keeps the sequence capturable in a HIP graph.  Each slot
     // holds [B, H] words in the forward and [B, 3H] in the backward.  A range
     // launch that continues the previous one keeps its slots (tags grow).
     if (zero_ws) {
         const size_t n_slots = (size_t)2 * a.B * (dir == 0 ? 1 : 3) * a.H;
-        const size_t n_xcc = a.xcc_words ? blocks : 0;
+        const size_t blocks = (size_t)c.groups * c.slices;
+        const size_t n_xcc = blocks <= (size_t)rec::MAX_XCC_BLOCKS ? blocks : 0;
         const size_t n = n_slots + n_xcc;
         hipLaunchKernelGGL(fill_u64_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
-                           stream, a.exch, n_slots, a.xcc_words, n_xcc, a.abort_flag);
+                           stream, a.exch, n_slots, xcc, n_xcc, a.abort_flag);
         RKA_RETURN_IF_HIP(hipGetLastError());
     }
-    a.xcc_tag = dir == 0 ? 1u : (unsigned)(a.T - a.t_end) + 1u;
     a.spin_limit = g_spin_limit.load();
-    if (c.kind == REC_REGISTER) return reg_launch(dir, c, a, stream);
-    return tiled_launch(dir, c, a, stream);
+    a.stall_block = g_stall_block.load();
+    return launch_slices(dir, c, a, xcc, stream);
 }
 
 }  // namespace

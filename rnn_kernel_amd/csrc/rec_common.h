@@ -8,8 +8,14 @@
 // start-up through the XCC_ID register), else an agent-scope one.  Two slots
 // (step parity) suffice because a writer can only reach step t+2 after every
 // reader of its group has published step t+1, i.e. finished reading step t.
-// Spins are bounded: on time-out a device flag is raised, every workgroup
-// leaves its time loop and writes its final state as NaN.
+//
+// Waits are bounded by a poll count (default 2^24 rounds, about 2 s at the
+// fastest poll rate; tests lower it from the host).  A wait that gives up
+// raises the launch's abort flag and
+// counts the launch in a per-device abort counter the host can read; every
+// workgroup then leaves its time loop, writes NaN into each output row it
+// did not store and NaN final states, so an aborted launch can only leave
+// values that are either NaN or the ones a complete run computes.
 #pragma once
 
 #include "rka_internal.h"
@@ -19,10 +25,23 @@ namespace rec {
 
 constexpr int NW = 8;          // wavefronts per workgroup
 constexpr int NTH = NW * 64;   // threads per workgroup
-// Poll rounds a bounded wait makes before it gives up (default; the
-// launch passes the limit in force, see rka_set_spin_limit).
-constexpr int SPIN_LIMIT = kDefaultSpinPolls;
 constexpr int MAX_XCC_BLOCKS = 4096;  // workgroups covered by the start-up XCD check
+
+// How a launch's waits give up.  `flag` is the call's abort flag
+// (workspace; shared by the launches of one call: batch slices, time
+// ranges), `count` the per-device counter of aborted calls; a wait
+// gives up after `spin_limit` poll rounds, or when it sees (every 1024
+// rounds) that another workgroup has raised the flag.  The bound is a poll
+// count rather than a clock: on MI355X a wall-clock check on the same
+// once-per-1024-rounds branch of the poll loop made a c2 backward launch 6 %
+// slower although the branch is never taken in a normal run.  Every grid is
+// resident (batch slices), so a wait lasts about one step unless other
+// kernels hold CUs the grid needs.
+struct WaitCtl {
+    int* flag;
+    unsigned long long* count;
+    int spin_limit;
+};
 
 // Host-side argument bundle of one recurrence launch.
 struct Args {
@@ -42,11 +61,16 @@ struct Args {
     float* reserve = nullptr;        // written by forward (nullable), read by backward
     unsigned long long* exch = nullptr;
     int* abort_flag = nullptr;
+    unsigned long long* abort_count = nullptr;  // per-device counter of aborted launches
     // one {xcc, tag} word per workgroup (nullptr: grid too large, exchange
     // through memory); tag distinct per launch on one workspace
     unsigned long long* xcc_words = nullptr;
     unsigned xcc_tag = 0;
-    int spin_limit = SPIN_LIMIT;  // poll rounds before a wait gives up
+    int spin_limit = 1 << 24;                 // poll rounds before a wait gives up
+    // Failure injection for tests (-1: off): the workgroup with this block
+    // index publishes every word into the other step-parity slot, where its
+    // partners never look for it, so their waits give up deterministically.
+    int stall_block = -1;
     int B = 0, T = 0, H = 0;
     // backward: steps t_end-1 down to t_begin of a sequence of T (strides and
     // exchange tags use the global step, so consecutive ranges continue one
@@ -122,6 +146,17 @@ __device__ __forceinline__ void publish_words(unsigned long long* const (&p)[N],
     }
 }
 
+// Raises the abort flag; the lane that raises it first counts the call in
+// the per-device abort counter (read by rka_recurrence_abort_count).
+__device__ __forceinline__ void raise_abort(const WaitCtl& wc) {
+    if (__hip_atomic_exchange(wc.flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 && wc.count != nullptr)
+        __hip_atomic_fetch_add(wc.count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool abort_raised(const WaitCtl& wc) {
+    return __hip_atomic_load(wc.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
 // Index of the XCD (accelerator complex die) this wavefront runs on.
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned v;
@@ -163,7 +198,7 @@ __device__ __forceinline__ GroupCoords group_coords(int G, int S) {
 // workspace.  Called by every thread of the workgroup (always contains a
 // barrier); words == nullptr answers false without an exchange.
 __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int first, int stride, int count,
-                                                 unsigned tag, int* abort_flag, int* s_flag, int spin_limit) {
+                                                 unsigned tag, const WaitCtl& wc, int* s_flag) {
     if (words == nullptr) {
         __syncthreads();
         return false;
@@ -181,10 +216,8 @@ __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int 
             unsigned long long w = load_word(p);
             int spins = 0;
             while ((unsigned)(w >> 32) != tag) {
-                if (++spins >= spin_limit ||
-                    ((spins & 1023) == 0 &&
-                     __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
-                    __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (++spins >= wc.spin_limit || ((spins & 1023) == 0 && abort_raised(wc))) {
+                    raise_abort(wc);
                     break;
                 }
                 w = load_word(p);
@@ -214,8 +247,7 @@ __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int 
 // wave of the grid would be a hot spot.
 template <int N>
 __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[N], const bool (&valid)[N],
-                                           unsigned long long (&w)[N], unsigned tag, int* abort_flag, int spin_limit,
-                                           bool& ok) {
+                                           unsigned long long (&w)[N], unsigned tag, const WaitCtl& wc, bool& ok) {
     auto ready = [&]() {
         bool r = true;
 #pragma unroll
@@ -241,12 +273,12 @@ __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[
         for (int v = 0; v < N; ++v) w[v] = load_word(p[v]);
         if (ready()) break;
         ++spins;
-        if (spins >= spin_limit) {
-            __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (spins >= wc.spin_limit) {
+            raise_abort(wc);
             give_up();
             break;
         }
-        if ((spins & 1023) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        if ((spins & 1023) == 0 && abort_raised(wc)) {
             give_up();
             break;
         }

@@ -439,10 +439,23 @@ int rka_set_backward_chunks(int chunks) {
 
 int rka_set_spin_limit(int polls) {
     clear_error();
-    if (polls < 0 || polls > kDefaultSpinPolls)
-        return fail(RKA_ERR_INVALID_ARGUMENT, "polls must be 0 (default) .. " + std::to_string(kDefaultSpinPolls));
+    if (polls < 0 || polls > kMaxSpinPolls)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "polls must be 0 (default, 2^24) .. " + std::to_string(kMaxSpinPolls));
     set_rec_spin_limit(polls);
     return 0;
+}
+
+int rka_set_stall_block(int block) {
+    clear_error();
+    if (block < -1) return fail(RKA_ERR_INVALID_ARGUMENT, "block must be -1 (off) or a workgroup index");
+    set_rec_stall_block(block);
+    return 0;
+}
+
+int rka_recurrence_abort_count(unsigned long long* count) {
+    clear_error();
+    if (!count) return fail(RKA_ERR_INVALID_ARGUMENT, "rka_recurrence_abort_count: null output pointer");
+    return rec_abort_count(count);
 }
 
 int rka_backward_chunks(int seq_len) {
@@ -454,16 +467,17 @@ int rka_backward_chunks(int seq_len) {
     return backward_chunks(seq_len);
 }
 
-int rka_describe_recurrence(int dir, int batch, int hidden_size, int out8[8]) {
+int rka_describe_recurrence(int dir, int batch, int hidden_size, int out10[10]) {
     clear_error();
-    if ((dir != 0 && dir != 1) || !out8) return fail(RKA_ERR_INVALID_ARGUMENT, "dir must be 0 or 1");
+    if ((dir != 0 && dir != 1) || !out10) return fail(RKA_ERR_INVALID_ARGUMENT, "dir must be 0 or 1");
     RKA_RETURN_IF_ERR(check_dims(batch, 1, 1, hidden_size));
     const DeviceInfo* dev = nullptr;
     RKA_RETURN_IF_ERR(current_device_info(&dev));
     RecConfig c{};
     RKA_RETURN_IF_ERR(choose_rec_config(dir, batch, hidden_size, *dev, &c));
-    const int v[8] = {c.kind, c.groups, c.slices, c.units, c.rows, c.pair_waves, c.chunk, c.lds_bytes};
-    for (int i = 0; i < 8; ++i) out8[i] = v[i];
+    const int v[10] = {c.kind,      c.groups, c.slices,    c.units,    c.rows,
+                       c.pair_waves, c.chunk, c.lds_bytes, c.launches, c.batch_per_launch};
+    for (int i = 0; i < 10; ++i) out10[i] = v[i];
     return 0;
 }
 

@@ -112,23 +112,39 @@ int choose_ksplit(int m, int n, int k, int num_cus, int wgs_per_cu);
 // ----------------------------------------------------------- recurrence ---
 enum RecKind { REC_AUTO = 0, REC_TILED = 1, REC_REGISTER = 2 };
 
+// A recurrence runs as `launches` kernel launches over consecutive batch
+// slices of `batch_per_launch` rows (the last one possibly shorter), each a
+// grid that is resident on an idle GPU: every workgroup of a launch can run
+// at once, so no exchange group waits for another group to finish.
 struct RecConfig {
     int kind = 0;          // REC_TILED or REC_REGISTER
-    int groups = 0;        // batch-row groups
+    int groups = 0;        // batch-row groups per launch (of a full slice)
     int slices = 0;        // hidden-unit slices
     int units = 0;         // hidden units per slice
     int rows = 0;          // batch rows per group
     int pair_waves = 0;    // tiled: wavefronts holding (row, unit) pairs
     int chunk = 0;         // register: k (forward) / j (backward) values per wavefront
     int lds_bytes = 0;     // dynamic LDS (tiled) or 0
+    int launches = 1;      // batch slices, one launch each
+    int batch_per_launch = 0;
 };
+// Batch rows per launch for a family whose grid of G groups of `rows` rows
+// and S slices holds at most `cap` resident workgroups (cap >= S): the whole
+// batch when it fits, else the most groups that fit, rounded down to a
+// multiple of 8 when that leaves at least 8 (groups then share an XCD).
+int batch_per_resident_launch(int batch, int rows, int S, long cap);
 int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, RecConfig* cfg);
 // Per-direction override used by rka_set_recurrence_config: kind, units, param.
 void set_rec_override(int dir, int kind, int units, int param);
-// Poll rounds a recurrence wait makes before it gives up (0: the default,
-// which is also the largest accepted value).
-constexpr int kDefaultSpinPolls = 1 << 21;
+// Poll rounds a recurrence wait makes before it gives up (the default, and
+// the largest value rka_set_spin_limit accepts).
+constexpr int kDefaultSpinPolls = 1 << 24;
+constexpr int kMaxSpinPolls = 1 << 30;
 void set_rec_spin_limit(int polls);
+void set_rec_stall_block(int block);
+// Number of recurrence launches on the current device that aborted since
+// the library was loaded (synchronises the device).
+int rec_abort_count(unsigned long long* count);
 
 size_t rec_workspace_bytes(int batch, int hidden);
 int eval_gate_functions(const float* x, float* sig, float* th, int n, hipStream_t stream);

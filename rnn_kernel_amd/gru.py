@@ -23,10 +23,25 @@ problems, ValueError for shapes and unsupported module options.
 Every tensor operation of the path is a call into librnn_kernel_amd.so; the
 only torch work here is allocation (the caching allocator owns all buffers)
 and the per-layer ``torch.cat`` of h_n, as in the reference.
+
+Failure of a recurrence launch: the kernels' waits are bounded, and a launch
+whose wait gave up leaves NaN in every output it did not compute (never a
+finite, wrong value) and is counted by the library.  The launches are
+asynchronous, so the count is read at synchronisation points:
+``check_recurrences()`` raises ``RecurrenceAbortedError`` (a RuntimeError) when
+it has grown since the previous check; with ``set_strict(True)`` (or the
+environment variable RKA_STRICT=1) every forward and backward call checks
+before returning, at the cost of a device synchronisation.  The reference
+raises before launching a grid it cannot make resident
+(src/rnn_kernel/a100/prod/gru.py:257-263); here such a batch is split into
+resident launches instead, and the check covers what remains: a wait that
+gives up.
 """
 from __future__ import annotations
 
 import math
+import os
+import threading
 from typing import Optional, Tuple
 
 import torch
@@ -35,7 +50,10 @@ import torch.nn as nn
 from . import _lib
 
 HIDDEN_SIZE = 256            # default hidden size, as in the reference module
-MAX_HIDDEN_SIZE = 1024
+# Largest hidden size accepted: the LDS-tiled backward (hidden_size > 256)
+# keeps at least 16 rows of 3H gate gradients in a workgroup's 160 KB of
+# LDS, which holds up to hidden_size 810 at batch >= 16.
+MAX_HIDDEN_SIZE = 768
 DEFAULT_NUM_LAYERS = 1
 
 
@@ -118,6 +136,39 @@ def _validate_inputs(x, h0, weight_ih, weight_hh, bias_ih, bias_hh) -> Tuple[int
     return batch, seq_len, input_size, hidden, index
 
 
+class RecurrenceAbortedError(RuntimeError):
+    """A recurrence launch gave up waiting for another workgroup; its outputs
+    hold NaN where they were not computed."""
+
+
+_abort_lock = threading.Lock()
+_abort_seen = {}  # device index -> abort count already reported
+_strict = os.environ.get("RKA_STRICT", "0") not in ("", "0")
+
+
+def set_strict(on: bool) -> None:
+    """When on, every GRUFunction forward / backward synchronises its device
+    and calls check_recurrences() before returning."""
+    global _strict
+    _strict = bool(on)
+
+
+def check_recurrences(device=None) -> None:
+    """Raise RecurrenceAbortedError if a recurrence call (one direction of
+    one layer) on ``device`` aborted since the previous check (synchronises
+    the device)."""
+    index = _device_index(device)
+    with torch.cuda.device(index):
+        count = _lib.recurrence_abort_count()
+    with _abort_lock:
+        seen = _abort_seen.get(index, 0)
+        _abort_seen[index] = count
+    if count > seen:
+        raise RecurrenceAbortedError(
+            f"{count - seen} GRU recurrence call(s) on cuda:{index} aborted (a wait for another workgroup "
+            "gave up); their outputs and gradients hold NaN")
+
+
 def _stream(device) -> int:
     return torch.cuda.current_stream(device=device).cuda_stream
 
@@ -146,6 +197,8 @@ def _run_forward(x, h0, weight_ih, weight_hh, bias_ih, bias_hh, training: bool):
             _lib.ptr(bias_hh), _lib.ptr(output), _lib.ptr(h_n), _lib.ptr(reserve), _lib.ptr(ws), ws_bytes,
             batch, seq_len, input_size, hidden, _stream(device))
         _lib.check(rc, "rka_gru_forward")
+    if _strict:
+        check_recurrences(index)
     return x, h0, weight_ih, weight_hh, output, h_n, reserve
 
 
@@ -191,6 +244,8 @@ class GRUFunction(torch.autograd.Function):
                 _lib.ptr(grad_w_ih), _lib.ptr(grad_w_hh), _lib.ptr(grad_b_ih), _lib.ptr(grad_b_hh),
                 _lib.ptr(ws), ws_bytes, batch, seq_len, input_size, hidden, _stream(device))
             _lib.check(rc, "rka_gru_backward")
+        if _strict:
+            check_recurrences(index)
         return grad_x, grad_h0, grad_w_ih, grad_w_hh, grad_b_ih, grad_b_hh
 
 

@@ -34,7 +34,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from .gru import GRU
+from .gru import GRU, check_recurrences
 from .train import AdamW, LinearHead, mse_loss
 
 IMPLEMENTATION = "rnn_kernel_amd"
@@ -211,6 +211,7 @@ def run_case(hidden_size: int, batches, args, device) -> BenchmarkResult:
                 last_loss = train_step(model, optimizer, x, y, loss_fn)
         torch.cuda.synchronize(device)
         elapsed = time.perf_counter() - start
+        check_recurrences(device)  # raises if a recurrence launch aborted
         ms_per_step = elapsed * 1000.0 / max(args.timed_steps, 1)
         avg = [s / counted for s in sums] if counted else [None] * 5
         steps_per_second = args.timed_steps / elapsed

@@ -117,8 +117,9 @@ LAYER_SHAPES = [
     (3, 6, 5, 200),      # four slices, the last one partial (float4 weight loads)
     (2, 5, 3, 221),      # four slices, H not a multiple of 4 (scalar weight loads)
     (4, 4, 2, 193),      # four slices, one unit in the last
-    (300, 3, 8, 256),    # B x 4 workgroups not resident: several rows per workgroup, launched in waves
+    (300, 3, 8, 256),    # B x 4 workgroups not resident: four rows per workgroup, two batch-slice launches
     (130, 4, 6, 130),    # three slices, two rows per workgroup
+    (400, 5, 4, 160),    # three slices at four rows not resident: batch-slice launches of 80 groups
 ]
 
 
@@ -152,12 +153,9 @@ def rec_kind(request, hip_lib):
         _lib.set_recurrence_config(d, 0, 0, 0)
 
 
-@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512)])
+@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768)])
 def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
     from rnn_kernel_amd import GRUFunction, _lib
-
-    if rec_kind == "tiled" and B >= 256:
-        pytest.skip("the LDS-tiled recurrences launch resident grids only; this batch needs waves")
 
     print(f"layer vs oracle B={B} T={T} I={I} H={H} kind={rec_kind} "
           f"fwd={_lib.describe_recurrence(0, B, H)} bwd={_lib.describe_recurrence(1, B, H)}", flush=True)
@@ -276,26 +274,40 @@ def test_recurrence_reserve_layout_matches_oracle_cache(gpu, oracle, hip_lib):
     assert _maxabs(y, f.y) <= 1e-5
 
 
-@pytest.mark.parametrize("B,T,H", [(16, 32, 256), (64, 24, 256), (6, 16, 130)])
-def test_timed_out_waits_abort_with_nan_final_states(gpu, oracle, hip_lib, rec_kind, B, T, H):
-    """Failure handling, forced from the host: with a one-poll limit
-    (rka_set_spin_limit) the recurrences' waits for other workgroups' words
-    give up, raise the launch's abort flag and end their time loops.  The
-    call still returns, the final states of aborted rows are NaN, and an
-    entry that stayed finite was computed from complete exchanges only, so
-    it equals the oracle's.  The next launch at the default limit zeroes
-    the flag with the exchange words and gives the oracle's results."""
+def _nan_or_equal(out, ref, name):
+    """Every entry of `out` is NaN or bitwise equal to `ref`; returns the NaN count."""
+    out, ref = out.detach().cpu(), ref.detach().cpu()
+    nan = torch.isnan(out)
+    assert not torch.isinf(out).any(), name
+    assert torch.equal(out[~nan], ref[~nan]), f"{name}: a finite entry differs from the complete run"
+    return int(nan.sum())
+
+
+@pytest.mark.parametrize("B,T,H", [(16, 32, 256), (64, 24, 256), (6, 16, 130), (300, 9, 256)])
+def test_timed_out_waits_abort_with_nan_in_every_unwritten_output(gpu, oracle, hip_lib, rec_kind, B, T, H):
+    """Failure handling, forced from the host: workgroup 0 of every launch
+    publishes its words where its partners never look (rka_set_stall_block)
+    and the poll bound is lowered to 256 rounds (rka_set_spin_limit), so the
+    partners' waits give up and the launch aborts, every kernel exiting
+    normally.  Every value an aborted launch leaves (y,
+    the reserve and hn of the forward; the gate-gradient rows G and dh0 of
+    the backward; dW, db and dx of a whole layer's backward) must be NaN or
+    bitwise equal to a complete run's, the complete run must equal the
+    oracle, and the per-device count of aborted calls
+    (rka_recurrence_abort_count) must grow by one per call, which
+    check_recurrences() turns into RecurrenceAbortedError."""
+    import rnn_kernel_amd
     from rnn_kernel_amd import _lib
 
-    p, x, h0, dy, dhn = _layer_inputs(B, T, 8, H, seed=B + T)
+    I = 8
+    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B + T)
     f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
                        p["bias_ih"].numpy(), p["bias_hh"].numpy())
     b = oracle.backward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(), f.y, f.cache,
                         dy.numpy(), dhn.numpy())
     gx = (x.double() @ p["weight_ih"].double().T + p["bias_ih"].double()).float().contiguous().to(gpu)
-    whh, bhh, h0d, dyd, dhnd = (t.contiguous().to(gpu) for t in (p["weight_hh"], p["bias_hh"], h0, dy, dhn))
-    y_ref = torch.as_tensor(f.y).float().to(gpu)
-    res_ref = torch.as_tensor(f.cache).float().to(gpu)
+    xd, wih, whh, bih, bhh, h0d, dyd, dhnd = (t.contiguous().to(gpu) for t in (
+        x, p["weight_ih"], p["weight_hh"], p["bias_ih"], p["bias_hh"], h0, dy, dhn))
     ws_bytes = hip_lib.rka_gru_recurrence_workspace_bytes(B, H)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
     stream = torch.cuda.current_stream().cuda_stream
@@ -303,42 +315,132 @@ def test_timed_out_waits_abort_with_nan_final_states(gpu, oracle, hip_lib, rec_k
     def forward():
         y = torch.empty(B, T, H, device=gpu)
         hn = torch.empty(B, H, device=gpu)
+        res = torch.empty(B, T, 4 * H, device=gpu)
         rc = hip_lib.rka_gru_recurrence_forward(gx.data_ptr(), h0d.data_ptr(), whh.data_ptr(), bhh.data_ptr(),
-                                                y.data_ptr(), hn.data_ptr(), None, ws.data_ptr(), ws_bytes,
-                                                B, T, H, stream)
+                                                y.data_ptr(), hn.data_ptr(), res.data_ptr(), ws.data_ptr(),
+                                                ws_bytes, B, T, H, stream)
         _lib.check(rc, "rka_gru_recurrence_forward")
         torch.cuda.synchronize()
-        return hn.cpu().double()
+        return y, hn, res
 
-    def backward():
+    def backward(y, res):
         g = torch.empty(B, T, 4 * H, device=gpu)
         dh0 = torch.empty(B, H, device=gpu)
-        rc = hip_lib.rka_gru_recurrence_backward(dyd.data_ptr(), dhnd.data_ptr(), res_ref.data_ptr(),
-                                                 h0d.data_ptr(), y_ref.data_ptr(), whh.data_ptr(), g.data_ptr(),
-                                                 dh0.data_ptr(), ws.data_ptr(), ws_bytes, B, T, H, stream)
+        rc = hip_lib.rka_gru_recurrence_backward(dyd.data_ptr(), dhnd.data_ptr(), res.data_ptr(), h0d.data_ptr(),
+                                                 y.data_ptr(), whh.data_ptr(), g.data_ptr(), dh0.data_ptr(),
+                                                 ws.data_ptr(), ws_bytes, B, T, H, stream)
         _lib.check(rc, "rka_gru_recurrence_backward")
         torch.cuda.synchronize()
-        return dh0.cpu().double()
+        return g, dh0
 
-    hn_ref, dh0_ref = torch.as_tensor(f.hn), torch.as_tensor(b.dh0)
+    def layer_backward(y, res):
+        lws = hip_lib.rka_gru_backward_workspace_bytes(B, T, I, H)
+        lw = torch.empty(lws, dtype=torch.uint8, device=gpu)
+        out = {k: torch.empty(*shape, device=gpu) for k, shape in (
+            ("dx", (B, T, I)), ("dh0", (B, H)), ("dw_ih", (3 * H, I)), ("dw_hh", (3 * H, H)),
+            ("db_ih", (3 * H,)), ("db_hh", (3 * H,)))}
+        rc = hip_lib.rka_gru_backward(xd.data_ptr(), h0d.data_ptr(), wih.data_ptr(), whh.data_ptr(), y.data_ptr(),
+                                      res.data_ptr(), dyd.data_ptr(), dhnd.data_ptr(), out["dx"].data_ptr(),
+                                      out["dh0"].data_ptr(), out["dw_ih"].data_ptr(), out["dw_hh"].data_ptr(),
+                                      out["db_ih"].data_ptr(), out["db_hh"].data_ptr(), lw.data_ptr(), lws,
+                                      B, T, I, H, stream)
+        _lib.check(rc, "rka_gru_backward")
+        torch.cuda.synchronize()
+        return out
+
     print(f"abort path: kind={rec_kind} B={B} T={T} H={H} fwd {_lib.describe_recurrence(0, B, H)} "
           f"bwd {_lib.describe_recurrence(1, B, H)}", flush=True)
+    rnn_kernel_amd.check_recurrences(gpu)  # earlier aborts are not this test's
+    # complete runs, pinned to the oracle
+    y_c, hn_c, res_c = forward()
+    g_c, dh0_c = backward(y_c, res_c)
+    layer_c = layer_backward(y_c, res_c)
+    assert _maxabs(y_c, f.y) <= OUT_ATOL and _maxabs(hn_c, f.hn) <= OUT_ATOL
+    assert _maxabs(res_c, f.cache) <= OUT_ATOL
+    assert _rel(dh0_c, b.dh0) <= GRAD_REL and _rel(layer_c["dw_hh"], b.dw_hh) <= GRAD_REL
+    assert _rel(layer_c["dx"], b.dx) <= GRAD_REL
+    rnn_kernel_amd.check_recurrences(gpu)
+    count0 = _lib.recurrence_abort_count()
     try:
-        _lib.set_spin_limit(1)
-        hn, dh0 = forward(), backward()
+        _lib.set_spin_limit(256)
+        _lib.set_stall_block(0)
+        y, hn, res = forward()
+        g, dh0 = backward(y_c, res_c)
+        layer = layer_backward(y_c, res_c)
     finally:
+        _lib.set_stall_block(-1)
         _lib.set_spin_limit(0)
-    for name, out, ref, tol in (("hn", hn, hn_ref, 1e-5), ("dh0", dh0, dh0_ref, GRAD_REL * float(dh0_ref.abs().max()))):
-        nan = torch.isnan(out)
-        print(f"  {name}: {int(nan.sum())} of {out.numel()} entries NaN", flush=True)
-        assert nan.any(), f"no {name} wait gave up after one poll"
-        assert not torch.isinf(out).any()
-        diff = (out - ref).abs()[~nan]
-        assert diff.numel() == 0 or float(diff.max()) <= tol
-    hn, dh0 = forward(), backward()
-    assert torch.isfinite(hn).all() and torch.isfinite(dh0).all()
-    assert float((hn - hn_ref).abs().max()) <= 1e-5
-    assert _rel(dh0, dh0_ref) <= GRAD_REL
+    nans = {
+        "y": _nan_or_equal(y, y_c, "y"), "reserve": _nan_or_equal(res, res_c, "reserve"),
+        "hn": _nan_or_equal(hn, hn_c, "hn"), "G": _nan_or_equal(g, g_c, "G"),
+        "dh0": _nan_or_equal(dh0, dh0_c, "dh0"),
+        **{f"layer {k}": _nan_or_equal(layer[k], layer_c[k], k) for k in layer},
+    }
+    print("  NaN entries after the forced aborts:", nans, flush=True)
+    for k in ("y", "reserve", "hn", "G", "dh0", "layer dh0", "layer dx"):
+        assert nans[k] > 0, f"{k}: the forced abort left no NaN"
+    # an aborted row leaves NaN G rows in every column of its slices, so the
+    # weight gradients, summed over all rows, cannot be finite
+    for k in ("dw_hh", "dw_ih", "db_hh", "db_ih"):
+        assert nans[f"layer {k}"] == layer[k].numel(), k
+    count1 = _lib.recurrence_abort_count()
+    assert count1 == count0 + 3, (count0, count1)  # one per aborted call, whatever its batch slices
+    with pytest.raises(rnn_kernel_amd.RecurrenceAbortedError):
+        rnn_kernel_amd.check_recurrences(gpu)
+    # the next launches at the default limit zero the flag with the exchange
+    # words and complete
+    y2, hn2, res2 = forward()
+    g2, dh02 = backward(y2, res2)
+    for a, c in ((y2, y_c), (hn2, hn_c), (res2, res_c), (g2, g_c), (dh02, dh0_c)):
+        assert torch.equal(a, c)
+    rnn_kernel_amd.check_recurrences(gpu)
+    assert _lib.recurrence_abort_count() == count1
+
+
+def test_strict_mode_raises_on_an_aborted_layer(gpu, hip_lib):
+    """set_strict(True): GRUFunction checks the abort count after its
+    launches; an abort forced from the host (rka_set_stall_block) then
+    raises RecurrenceAbortedError from the forward call itself."""
+    import rnn_kernel_amd
+    from rnn_kernel_amd import GRU, _lib
+
+    torch.manual_seed(3)
+    model = GRU(8, 256).to(gpu)
+    x = torch.randn(16, 24, 8, device=gpu)
+    rnn_kernel_amd.check_recurrences(gpu)
+    rnn_kernel_amd.set_strict(True)
+    try:
+        y, hn = model(x)  # complete: no error
+        _lib.set_spin_limit(256)
+        _lib.set_stall_block(0)
+        with pytest.raises(rnn_kernel_amd.RecurrenceAbortedError):
+            model(x)
+    finally:
+        _lib.set_stall_block(-1)
+        _lib.set_spin_limit(0)
+        rnn_kernel_amd.set_strict(False)
+    y2, hn2 = model(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2) and torch.equal(hn, hn2)
+    rnn_kernel_amd.check_recurrences(gpu)
+
+
+@pytest.mark.parametrize("B,H,launches", [(300, 256, 2), (400, 160, 2), (64, 256, 1)])
+def test_batch_slices_of_resident_launches(gpu, hip_lib, B, H, launches):
+    """A batch whose grid would not be resident runs as launches over batch
+    slices, each resident (the largest count of groups that fits, a multiple
+    of 8 so groups share an XCD); the described split covers the batch."""
+    from rnn_kernel_amd import _lib
+
+    for d in (0, 1):
+        desc = _lib.describe_recurrence(d, B, H)
+        print(f"dir {d} B={B} H={H}: {desc}", flush=True)
+        assert desc["launches"] == launches
+        per = desc["batch_per_launch"]
+        assert (desc["launches"] - 1) * per < B <= desc["launches"] * per
+        assert desc["groups"] == -(-per // desc["rows"])
+        if launches > 1:
+            assert desc["groups"] % 8 == 0
 
 
 @pytest.mark.parametrize("B,H,local", [(64, 256, True), (8, 256, True), (4, 256, False), (3, 130, False)])

@@ -64,7 +64,10 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     assert hip_lib.rka_set_backward_chunks(-1) == 1001
     assert hip_lib.rka_set_backward_chunks(9) == 1001
     assert hip_lib.rka_set_spin_limit(-1) == 1001
-    assert hip_lib.rka_set_spin_limit((1 << 21) + 1) == 1001   # above the default
+    assert hip_lib.rka_set_spin_limit((1 << 30) + 1) == 1001   # above the largest poll bound
+    assert hip_lib.rka_recurrence_abort_count(None) == 1001
+    assert hip_lib.rka_set_stall_block(-2) == 1001
+    assert hip_lib.rka_set_stall_block(-1) == 0
     assert hip_lib.rka_set_spin_limit(0) == 0
     assert hip_lib.rka_backward_chunks(0) == -1
 
