@@ -123,6 +123,24 @@ int rka_gru_recurrence_forward(const float* gx, const float* h0,
                                int batch, int seq_len, int hidden_size,
                                void* stream);
 
+/* The same as rka_gru_recurrence_forward without a workspace, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  The exchange state lives in a static device array of the
+ * library, one per GPU (4 MiB + 32 KiB + 256 B, held until the process
+ * ends; set up on the first call on each device); the call allocates no
+ * device memory.  Limit: batch * hidden_size <= 262144 (2 B H 8-byte
+ * words in 4 MiB); larger shapes return RKA_ERR_UNSUPPORTED_SHAPE without
+ * launching.  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams or threads without ordering) race
+ * and give wrong results; calls ordered on one stream are safe (each zeroes
+ * the state it uses first). */
+int rka_gru_recurrence_forward_noalloc(const float* gx, const float* h0,
+                                       const float* w_hh, const float* b_hh,
+                                       float* y, float* hn, float* reserve,
+                                       int batch, int seq_len, int hidden_size,
+                                       void* stream);
+
 /* Persistent reverse-time recurrence.  Writes the gate gradients
  * g [B,T,4H] as blocks (da_n, dr^, dz^, dn^) and dh0.  dy / dhn may be NULL.
  * Replaces _launch_backward_sequence (src/rnn_kernel/a100/prod/gru.py:415-487),

@@ -31,6 +31,7 @@ SIGNATURES = {
     "rka_gemm_f32": (_I, [_I, _I, _I, _P, _I, _I, _P, _I, _I, _P, _P, _I, _P]),
     "rka_gru_recurrence_workspace_bytes": (_SZ, [_I, _I]),
     "rka_gru_recurrence_forward": (_I, [_P] * 7 + [_P, _SZ, _I, _I, _I, _P]),
+    "rka_gru_recurrence_forward_noalloc": (_I, [_P] * 7 + [_I, _I, _I, _P]),
     "rka_gru_recurrence_backward": (_I, [_P] * 8 + [_P, _SZ, _I, _I, _I, _P]),
     "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
     "rka_set_backward_chunks": (_I, [_I]),

@@ -159,21 +159,27 @@ int launch_slices(int dir, const RecConfig& c, rec::Args a, unsigned long long* 
     return 0;
 }
 
-int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipStream_t stream) {
+// Where a launch's exchange state lives: the two slots of words, the
+// start-up XCD words and the abort flag.
+struct RecState {
+    unsigned long long* exch;
+    unsigned long long* xcc;
+    int* flag;
+};
+
+// Launches direction `dir` with its exchange state at `st` (zeroed first
+// when zero_ws; a backward range that continues the previous one keeps it).
+int launch_at(int dir, rec::Args& a, const RecState& st, bool zero_ws, hipStream_t stream) {
     const DeviceInfo* dev = nullptr;
     RKA_RETURN_IF_ERR(current_device_info(&dev));
     RecConfig c{};
     RKA_RETURN_IF_ERR(choose_rec_config(dir, a.B, a.H, *dev, &c));
-    const size_t need = rec_workspace_bytes(a.B, a.H);
-    if (ws == nullptr || ws_bytes < need)
-        return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "recurrence workspace too small: need " + std::to_string(need) +
-                                                     " bytes, got " + std::to_string(ws_bytes));
     if ((size_t)a.T * c.launches + c.launches >= 0xffffffffull)
         return fail(RKA_ERR_UNSUPPORTED_SHAPE, "recurrence: seq_len times batch slices exceeds the 32-bit step tags");
-    a.exch = reinterpret_cast<unsigned long long*>(ws);
-    a.abort_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + need - 256);
+    a.exch = st.exch;
+    a.abort_flag = st.flag;
     RKA_RETURN_IF_ERR(abort_counter(dev->device, &a.abort_count));
-    unsigned long long* xcc = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + slots_bytes(a.B, a.H));
+    unsigned long long* xcc = st.xcc;
     // Tags start at 1, so zeroed words never match; a fill kernel (not a
     // memset node) keeps the sequence capturable in a HIP graph.  Each slot
     // holds [B, H] words in the forward and [B, 3H] in the backward.  A range
@@ -190,6 +196,45 @@ int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipSt
     a.spin_limit = g_spin_limit.load();
     a.stall_block = g_stall_block.load();
     return launch_slices(dir, c, a, xcc, stream);
+}
+
+int launch(int dir, rec::Args& a, void* ws, size_t ws_bytes, bool zero_ws, hipStream_t stream) {
+    const size_t need = rec_workspace_bytes(a.B, a.H);
+    if (ws == nullptr || ws_bytes < need)
+        return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "recurrence workspace too small: need " + std::to_string(need) +
+                                                     " bytes, got " + std::to_string(ws_bytes));
+    char* base = reinterpret_cast<char*>(ws);
+    const RecState st{reinterpret_cast<unsigned long long*>(base),
+                      reinterpret_cast<unsigned long long*>(base + slots_bytes(a.B, a.H)),
+                      reinterpret_cast<int*>(base + need - 256)};
+    return launch_at(dir, a, st, zero_ws, stream);
+}
+
+// ------------------------------------------- allocation-free forward ---
+// Exchange state of rka_gru_recurrence_forward_noalloc: a file-scope device
+// array, one per GPU, held until the process ends.  Layout: the forward's
+// two slots of [B, H] words (at most kNoAllocSlotBytes), then the start-up
+// XCD words, then the abort flag.  The array's name is a host-side
+// stand-in, not a device address: host code uses only the address that
+// hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocSlotBytes = size_t(4) << 20;
+constexpr size_t kNoAllocXccBytes = (size_t)rec::MAX_XCC_BLOCKS * sizeof(unsigned long long);
+constexpr size_t kNoAllocScratchBytes = kNoAllocSlotBytes + kNoAllocXccBytes + 256;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mutex;
+std::vector<char*> g_scratch_ptr;  // per device: device address of `scratch`
+
+int scratch_address(int dev, char** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        RKA_RETURN_IF_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch_ptr[dev] = reinterpret_cast<char*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
 }
 
 }  // namespace
@@ -210,6 +255,39 @@ int eval_gate_functions(const float* x, float* sig, float* th, int n, hipStream_
     hipLaunchKernelGGL(eval_gate_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, sig, th, n);
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
+}
+
+size_t rec_noalloc_max_slot_bytes() { return kNoAllocSlotBytes; }
+
+int launch_rec_forward_noalloc(const float* gx, const float* h0, const float* w_hh, const float* b_hh, float* y,
+                               float* hn, float* reserve, int B, int T, int H, hipStream_t stream) {
+    const size_t slot_bytes = align_up((size_t)2 * B * H * sizeof(unsigned long long), 256);
+    if (slot_bytes > kNoAllocSlotBytes)
+        return fail(RKA_ERR_UNSUPPORTED_SHAPE,
+                    "rka_gru_recurrence_forward_noalloc: batch * hidden_size = " + std::to_string((size_t)B * H) +
+                        " exceeds the static scratch limit of " + std::to_string(kNoAllocSlotBytes / 16) +
+                        " (use rka_gru_recurrence_forward with a workspace)");
+    const DeviceInfo* dev = nullptr;
+    RKA_RETURN_IF_ERR(current_device_info(&dev));
+    char* ptr = nullptr;
+    RKA_RETURN_IF_ERR(scratch_address(dev->device, &ptr));
+    const RecState st{reinterpret_cast<unsigned long long*>(ptr),
+                      reinterpret_cast<unsigned long long*>(ptr + kNoAllocSlotBytes),
+                      reinterpret_cast<int*>(ptr + kNoAllocSlotBytes + kNoAllocXccBytes)};
+    rec::Args a;
+    a.gx = gx;
+    a.h0 = h0;
+    a.w_hh = w_hh;
+    a.b_hh = b_hh;
+    a.y = y;
+    a.hn = hn;
+    a.reserve = reserve;
+    a.B = B;
+    a.T = T;
+    a.H = H;
+    a.t_begin = 0;
+    a.t_end = T;
+    return launch_at(0, a, st, true, stream);
 }
 
 int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,

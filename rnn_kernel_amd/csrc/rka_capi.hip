@@ -396,6 +396,17 @@ int rka_gru_recurrence_forward(const float* gx, const float* h0, const float* w_
                               hidden_size, reinterpret_cast<hipStream_t>(stream));
 }
 
+int rka_gru_recurrence_forward_noalloc(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
+                                       float* y, float* hn, float* reserve, int batch, int seq_len, int hidden_size,
+                                       void* stream) {
+    clear_error();
+    RKA_RETURN_IF_ERR(check_dims(batch, seq_len, 1, hidden_size));
+    if (!gx || !h0 || !w_hh || !b_hh || !y || !hn)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "rka_gru_recurrence_forward_noalloc: null tensor pointer");
+    return launch_rec_forward_noalloc(gx, h0, w_hh, b_hh, y, hn, reserve, batch, seq_len, hidden_size,
+                                      reinterpret_cast<hipStream_t>(stream));
+}
+
 int rka_gru_recurrence_backward(const float* dy, const float* dhn, const float* reserve, const float* h0,
                                 const float* y, const float* w_hh, float* g, float* dh0, void* workspace,
                                 size_t workspace_bytes, int batch, int seq_len, int hidden_size, void* stream) {

@@ -152,6 +152,11 @@ int eval_gate_functions(const float* x, float* sig, float* th, int n, hipStream_
 int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
                        float* y, float* hn, float* reserve, void* ws, size_t ws_bytes,
                        int B, int T, int H, hipStream_t stream);
+// The same with the exchange state in a static per-device array (no
+// workspace); 2 B H words at most rec_noalloc_max_slot_bytes() / 8.
+int launch_rec_forward_noalloc(const float* gx, const float* h0, const float* w_hh, const float* b_hh, float* y,
+                               float* hn, float* reserve, int B, int T, int H, hipStream_t stream);
+size_t rec_noalloc_max_slot_bytes();
 int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,
                         const float* h0, const float* y, const float* w_hh,
                         float* g, float* dh0, void* ws, size_t ws_bytes,

@@ -1,0 +1,72 @@
+"""The allocation-free forward recurrence (rka_gru_recurrence_forward_noalloc)
+against the workspace entry point it mirrors (rka_gru_recurrence_forward):
+bitwise-equal y, hn and reserve on two calls in a row, the second smaller,
+each run through the C ABI on the same inputs."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, T, H, seed, gpu):
+    g = torch.Generator().manual_seed(seed)
+    k = H ** -0.5
+    gx = torch.randn(B, T, 3 * H, generator=g).to(gpu)
+    whh = ((torch.rand(3 * H, H, generator=g) * 2 - 1) * k).to(gpu)
+    bhh = ((torch.rand(3 * H, generator=g) * 2 - 1) * k).to(gpu)
+    h0 = (0.5 * torch.randn(B, H, generator=g)).to(gpu)
+    return gx, whh, bhh, h0
+
+
+def _outputs(B, T, H, gpu, with_reserve):
+    y = torch.full((B, T, H), float("nan"), device=gpu)
+    hn = torch.full((B, H), float("nan"), device=gpu)
+    res = torch.full((B, T, 4 * H), float("nan"), device=gpu) if with_reserve else None
+    return y, hn, res
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+@pytest.mark.parametrize("with_reserve", [True, False])
+def test_noalloc_forward_matches_workspace_forward(gpu, hip_lib, with_reserve):
+    from rnn_kernel_amd import _lib
+
+    stream = torch.cuda.current_stream().cuda_stream
+    # two calls in a row on the shared static state, the second smaller
+    for B, T, H, seed in ((64, 40, 256, 1), (5, 7, 130, 2)):
+        print(f"noalloc forward B={B} T={T} H={H} reserve={with_reserve}", flush=True)
+        gx, whh, bhh, h0 = _inputs(B, T, H, seed, gpu)
+        y_ref, hn_ref, res_ref = _outputs(B, T, H, gpu, with_reserve)
+        ws_bytes = hip_lib.rka_gru_recurrence_workspace_bytes(B, H)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
+        rc = hip_lib.rka_gru_recurrence_forward(gx.data_ptr(), h0.data_ptr(), whh.data_ptr(), bhh.data_ptr(),
+                                                y_ref.data_ptr(), hn_ref.data_ptr(), _ptr(res_ref), ws.data_ptr(),
+                                                ws_bytes, B, T, H, stream)
+        _lib.check(rc, "rka_gru_recurrence_forward")
+        y, hn, res = _outputs(B, T, H, gpu, with_reserve)
+        rc = hip_lib.rka_gru_recurrence_forward_noalloc(gx.data_ptr(), h0.data_ptr(), whh.data_ptr(),
+                                                        bhh.data_ptr(), y.data_ptr(), hn.data_ptr(), _ptr(res),
+                                                        B, T, H, stream)
+        _lib.check(rc, "rka_gru_recurrence_forward_noalloc")
+        torch.cuda.synchronize()
+        assert torch.isfinite(y_ref).all() and torch.isfinite(hn_ref).all()
+        assert torch.equal(y, y_ref)
+        assert torch.equal(hn, hn_ref)
+        if with_reserve:
+            assert torch.equal(res, res_ref)
+
+
+def test_noalloc_forward_rejects_shapes_beyond_its_static_scratch(gpu, hip_lib):
+    """batch * hidden_size above 262144 is refused before anything launches."""
+    from rnn_kernel_amd import _lib
+
+    B, T, H = 2048, 2, 256
+    dummy = torch.zeros(16, device=gpu)
+    p = dummy.data_ptr()
+    rc = hip_lib.rka_gru_recurrence_forward_noalloc(p, p, p, p, p, p, None, B, T, H,
+                                                    torch.cuda.current_stream().cuda_stream)
+    assert rc == 1004  # RKA_ERR_UNSUPPORTED_SHAPE
+    assert "static scratch limit" in _lib.last_error()
+    torch.cuda.synchronize()
