@@ -10,13 +10,24 @@ reference's published fwd+bwd numbers).  The MSE loss is the library's
 torch.nn.GRU baselines use F.mse_loss.  Inputs are generated on the CPU with
 seed 42, copied to the GPU, and resident in HBM before timing starts.
 
+Timing protocol (the reference's, rnn_benchmark.py:642-694, with hip events):
+W untimed warm-up steps, then K timed steps bracketed by
+torch.cuda.synchronize(); an event is recorded on the stream after every
+step, and ms_per_step is the MEDIAN of the K per-step times (the wall-clock
+mean over the K steps is reported beside it).
+
 Prints ONE JSON line (rank 0).  Besides the contract fields it carries:
-  roofline      - the dominant kernel's achieved vs peak rate, from the
-                  library's own per-stage hipEvent timing of the timed steps;
-  cpu_baseline  - the C oracle (fp32, one thread) on a bounded sample of the
-                  same workload (fewer timesteps), timed on this host;
-  torch_gru_gpu - torch.nn.GRU (MIOpen/rocBLAS) on the same GPU, same protocol;
-  torch_gru_cpu - torch.nn.GRU on this host's CPU cores, bounded sample.
+  roofline      - the dominant kernel (the slower recurrence): achieved rate
+                  from the library's own per-stage hipEvents on the launch
+                  stream over a separate pass of K steps, against the fp32
+                  peak and, as a latency-bound kernel, against the measured
+                  floor of its step structure;
+  cpu_baseline  - torch.nn.GRU fp32 on this host's CPU cores (the
+                  reference's CPU path), full workload, 1 warm-up + 5 timed
+                  steps, median; thread count, CPU model and MKL / oneDNN
+                  versions recorded;
+  cpu_oracle_port - the C oracle (fp32, one thread), bounded sample;
+  torch_gru_gpu - torch.nn.GRU (MIOpen/rocBLAS) on the same GPU, same protocol.
 """
 from __future__ import annotations
 
@@ -34,7 +45,16 @@ METRIC = "fp32 GRU fwd+bwd timesteps/sec & µs/step, H=256 B=64 T=512, 1 MI355X"
 B, T, I, H, L = 64, 512, 256, 256, 1
 SEED = 42
 MFMA_FP32_PEAK_TFLOPS = 157.3
+VALU_FP32_PEAK_TFLOPS = 78.6   # non-packed fp32 FMA (packed fp32 is disabled in this build)
 HBM_PEAK_GBS = 8000.0
+# Measured floor of the recurrences' step structure at c2, microseconds per
+# timestep: a timing copy of each kernel that keeps the exchange, both
+# barriers, the LDS broadcasts and reductions and the gate math but drops the
+# W_hh FMAs and the owner's per-step output stores and input loads (MI355X,
+# mean of two runs: forward 0.3333 / 0.3292 ms, backward 0.3499 / 0.3486 ms
+# per T = 512 launch).  The timing copy is not shipped.
+STEP_FLOOR_US = {"forward_recurrence": 0.647, "backward_recurrence": 0.682}
+CPU_THREAD_CAP = 16  # the GPU box's CPU share for one GPU, whatever os.cpu_count() reports
 
 
 def flops_per_step(B, T, I, H):
@@ -92,6 +112,9 @@ def make_inputs():
 
 
 def time_steps(model, x, h0, target, steps, warmup, sync, profile_cb=None, loss_fn=None):
+    """(median per-step seconds from stream events, wall-clock mean seconds)
+    of `steps` timed steps after `warmup` untimed ones."""
+    import torch
     import torch.nn.functional as F
 
     loss_fn = loss_fn or F.mse_loss
@@ -110,12 +133,16 @@ def time_steps(model, x, h0, target, steps, warmup, sync, profile_cb=None, loss_
     sync()
     if profile_cb:
         profile_cb(True)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    for _ in range(steps):
+    events[0].record()
+    for i in range(steps):
         step()
+        events[i + 1].record()
     sync()
     elapsed = time.perf_counter() - t0
-    return elapsed / steps
+    per_step = [events[i].elapsed_time(events[i + 1]) * 1e-3 for i in range(steps)]
+    return statistics.median(per_step), elapsed / steps
 
 
 # The other BASELINE configs, measured with `--workload` (the default run is c2
@@ -245,6 +272,65 @@ def run_other_workload(name, args):
     print(json.dumps(result), flush=True)
 
 
+def cpu_identity():
+    """CPU model, logical CPUs and the BLAS / oneDNN builds torch uses."""
+    import torch
+
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    cfg = torch.__config__.show()
+    mkl = next((ln.strip() for ln in cfg.splitlines() if "Math Kernel Library" in ln or "oneMKL" in ln), None)
+    onednn = next((ln.strip() for ln in cfg.splitlines() if "oneDNN" in ln or "MKL-DNN" in ln), None)
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "mkl": mkl, "onednn": onednn,
+            "torch": torch.__version__}
+
+
+def torch_cpu_baseline(runs: int = 5):
+    """torch.nn.GRU fp32 fwd+bwd (MSE loss) on the host CPU at the full c2
+    workload: 1 warm-up + `runs` timed runs with time.perf_counter, median
+    (rnn_benchmark.py:674-694)."""
+    import torch
+    import torch.nn.functional as F
+
+    threads = min(os.cpu_count() or 1, CPU_THREAD_CAP)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        gru, x, h0, target = make_inputs()
+        times = []
+        for i in range(runs + 1):
+            xs = x.clone().requires_grad_(True)
+            hs = h0.clone().requires_grad_(True)
+            gru.zero_grad(set_to_none=True)
+            t0 = time.perf_counter()
+            out, _ = gru(xs, hs)
+            F.mse_loss(out, target).backward()
+            dt = time.perf_counter() - t0
+            if i > 0:
+                times.append(dt)
+    finally:
+        torch.set_num_threads(prev)
+    med = statistics.median(times)
+    return {
+        "value": T / med,
+        "unit": "timesteps/s",
+        "cores": threads,
+        "kind": "reference",
+        "ms_per_step": med * 1e3,
+        "runs_ms": [round(t * 1e3, 2) for t in times],
+        "sample": (f"torch.nn.GRU fp32 fwd+bwd + MSE on the host CPU, full workload B={B} T={T} I={I} H={H}, "
+                   f"1 warm-up + {runs} timed runs, median; {threads} threads (the box's CPU share for one GPU "
+                   f"is {CPU_THREAD_CAP}, whatever os.cpu_count() reports)"),
+        "host": cpu_identity(),
+    }
+
+
 def cpu_oracle_baseline(budget_s: float):
     """C oracle (fp32, single thread) on the c2 shape with fewer timesteps."""
     import numpy as np
@@ -276,36 +362,13 @@ def cpu_oracle_baseline(budget_s: float):
     }
 
 
-def torch_cpu_baseline(budget_s: float):
-    import torch
-    import torch.nn.functional as F
-
-    # the GPU box's CPU share is 16 threads whatever os.cpu_count() reports
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")))
-    torch.set_num_threads(threads)
-    gru, x, h0, target = make_inputs()
-    t_sample = 16
-    while True:
-        xs = x[:, :t_sample].clone().requires_grad_(True)
-        hs = h0.clone().requires_grad_(True)
-        t0 = time.perf_counter()
-        out, _ = gru(xs, hs)
-        F.mse_loss(out, target[:, :t_sample]).backward()
-        dt = time.perf_counter() - t0
-        if dt * 4 > budget_s or t_sample >= T:
-            break
-        t_sample = min(T, t_sample * 4)
-    return {"value": t_sample / dt, "unit": "timesteps/s", "threads": threads,
-            "sample": f"torch.nn.GRU fp32 CPU fwd+bwd, T={t_sample} of {T}, {dt:.2f} s"}
-
-
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--cpu-budget", type=float, default=30.0,
-                        help="upper bound (s) of one CPU baseline sample; samples grow x4 in timesteps while "
+    parser.add_argument("--cpu-budget", type=float, default=20.0,
+                        help="upper bound (s) of the C oracle's sample; samples grow x4 in timesteps while "
                              "the next one fits")
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--skip-torch-gpu", action="store_true")
@@ -323,7 +386,7 @@ def main():
 
     import torch
 
-    from rnn_kernel_amd import _lib, from_torch_gru, mse_loss
+    from rnn_kernel_amd import _lib, check_recurrences, from_torch_gru, mse_loss
 
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
@@ -337,14 +400,14 @@ def main():
     target = target_cpu.to(dev)
     ours = from_torch_gru(gru.to(dev))
 
+    # pass 1: per-stage library events (roofline and stage split)
     _lib.profile_read()  # clear
-    t_step = time_steps(ours, x, h0, target, args.steps, args.warmup, sync, profile_cb=_lib.profile_enable,
-                        loss_fn=mse_loss)
+    time_steps(ours, x, h0, target, args.steps, args.warmup, sync, profile_cb=_lib.profile_enable, loss_fn=mse_loss)
     stages = _lib.profile_read()
     _lib.profile_enable(False)
-    # second timed pass without event records for the headline number
-    t_step_noprof = time_steps(ours, x, h0, target, args.steps, 0, sync, loss_fn=mse_loss)
-    t_step = min(t_step, t_step_noprof)
+    # pass 2, the headline: no stage events, one event per step boundary
+    t_step, t_wall = time_steps(ours, x, h0, target, args.steps, 2, sync, loss_fn=mse_loss)
+    check_recurrences()  # raises if a recurrence call aborted
 
     # per-step stage totals; a stage may run as several launches per step
     # (the backward recurrence in time chunks), and side-stream GEMM stages
@@ -368,6 +431,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": t_step * 1e3,
+        "wall_ms_per_step_mean": t_wall * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -384,15 +448,22 @@ def main():
         "launches_per_step": {k: round(v, 2) for k, v in launches.items()},
         "roofline": {
             "kernel": dominant,
-            "bound": "mfma",
+            "bound": "latency" if dominant in STEP_FLOOR_US else "mfma",
             "achieved": achieved,
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
             "traffic": measured_traffic(dominant),
-            "note": ("serial recurrence, latency-bound (one cross-workgroup exchange per timestep); achieved = "
-                     "algorithmic FLOPs / mean launch time from hipEvents on the launch stream; traffic = "
-                     "copy-calibrated FETCH_SIZE+WRITE_SIZE bytes per launch from the committed rocprofv3 summary"),
+            "note": ("serial recurrence: VALU FMAs (no MFMA) between one cross-workgroup exchange per timestep, "
+                     "latency-bound; achieved = algorithmic FLOPs / mean launch time from hipEvents on the launch "
+                     "stream; frac against the published fp32 peak, valu_frac against the non-packed fp32 VALU "
+                     "peak, floor_frac = measured step-structure floor / measured step; traffic = copy-calibrated "
+                     "FETCH_SIZE+WRITE_SIZE bytes per launch from the committed rocprofv3 summary"),
+            "valu_peak": VALU_FP32_PEAK_TFLOPS,
+            "valu_frac": achieved / VALU_FP32_PEAK_TFLOPS,
+            "floor_us_per_timestep": STEP_FLOOR_US.get(dominant),
+            "floor_frac": (STEP_FLOOR_US[dominant] / (stage_step[dominant] * 1e3 / T / per_launch))
+            if dominant in STEP_FLOOR_US else None,
             "us_per_timestep": stage_step[dominant] * 1e3 / T,
             "launch_ms": dom_ms,
             "launches_per_step": per_launch,
@@ -405,12 +476,12 @@ def main():
         gru_gpu = gru.to(dev)
         gru_gpu.flatten_parameters()
         x.grad = None
-        t_torch = time_steps(gru_gpu, x, h0, target, max(3, args.steps // 2), 2, sync)
+        t_torch, _ = time_steps(gru_gpu, x, h0, target, max(3, args.steps // 2), 2, sync)
         result["torch_gru_gpu"] = {"value": T / t_torch, "unit": "timesteps/s", "ms_per_step": t_torch * 1e3,
                                    "speedup_of_ours": t_torch / t_step}
     if not args.skip_cpu:
-        result["cpu_baseline"] = cpu_oracle_baseline(args.cpu_budget)
-        result["torch_gru_cpu"] = torch_cpu_baseline(args.cpu_budget)
+        result["cpu_baseline"] = torch_cpu_baseline()
+        result["cpu_oracle_port"] = cpu_oracle_baseline(args.cpu_budget)
     print(json.dumps(result), flush=True)
 
 

@@ -128,6 +128,53 @@ def backward(x, h0, w_ih, w_hh, y, cache, dy, dhn, dtype=np.float64, need_dx: bo
     return BackwardResult(dx, dh0, dw_ih, dw_hh, db_ih, db_hh)
 
 
+def _row_chunks(B: int, threads: int):
+    n = max(1, min(int(threads), B))
+    edges = [B * k // n for k in range(n + 1)]
+    return [(edges[k], edges[k + 1]) for k in range(n) if edges[k + 1] > edges[k]]
+
+
+def forward_rows_parallel(x, h0, w_ih, w_hh, b_ih, b_hh, threads: int, dtype=np.float64) -> ForwardResult:
+    """``forward`` with the batch rows split over ``threads`` threads.
+
+    Batch rows are independent sequences, so every row's result is the one
+    ``forward`` computes for it (the C calls release the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    x, h0 = np.asarray(x), np.asarray(h0)
+    chunks = _row_chunks(x.shape[0], threads)
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        parts = list(ex.map(lambda c: forward(x[c[0]:c[1]], h0[c[0]:c[1]], w_ih, w_hh, b_ih, b_hh, dtype=dtype),
+                            chunks))
+    return ForwardResult(np.concatenate([f.y for f in parts]), np.concatenate([f.hn for f in parts]),
+                         np.concatenate([f.cache for f in parts]))
+
+
+def backward_rows_parallel(x, h0, w_ih, w_hh, y, cache, dy, dhn, threads: int, dtype=np.float64) -> BackwardResult:
+    """``backward`` with the batch rows split over ``threads`` threads: dx and
+    dh0 rows are the per-row results, and the weight and bias gradients are
+    the chunks' sums added in chunk order (the same sums as ``backward``,
+    grouped by chunk)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    x, h0, y, cache = np.asarray(x), np.asarray(h0), np.asarray(y), np.asarray(cache)
+    chunks = _row_chunks(x.shape[0], threads)
+
+    def run(c):
+        a, b = c
+        return backward(x[a:b], h0[a:b], w_ih, w_hh, y[a:b], cache[a:b], None if dy is None else np.asarray(dy)[a:b],
+                        None if dhn is None else np.asarray(dhn)[a:b], dtype=dtype)
+
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        parts = list(ex.map(run, chunks))
+    acc = {k: getattr(parts[0], k).copy() for k in ("dw_ih", "dw_hh", "db_ih", "db_hh")}
+    for part in parts[1:]:
+        for k in acc:
+            acc[k] += getattr(part, k)
+    return BackwardResult(np.concatenate([b.dx for b in parts]), np.concatenate([b.dh0 for b in parts]),
+                          acc["dw_ih"], acc["dw_hh"], acc["db_ih"], acc["db_hh"])
+
+
 @dataclass
 class StackResult:
     y: np.ndarray                 # [B, T, H] output of the last layer

@@ -178,3 +178,26 @@ def test_oracle_none_gradients_mean_zero(oracle):
     b = oracle.backward(x, h0, p["weight_ih"], p["weight_hh"], f.y, f.cache, np.zeros((B, T, H)), dhn)
     np.testing.assert_array_equal(a.dx, b.dx)
     np.testing.assert_array_equal(a.dw_hh, b.dw_hh)
+
+
+def test_row_parallel_oracle_equals_the_single_call():
+    """The batch-row-parallel wrappers (used for the full-size parity check)
+    give the single call's per-row results exactly and its weight gradients
+    up to the grouping of the batch sum."""
+    from oracle import gru_oracle
+
+    rng = np.random.default_rng(11)
+    B, T, I, H = 7, 5, 4, 6
+    k = H ** -0.5
+    w_ih, w_hh = rng.uniform(-k, k, (3 * H, I)), rng.uniform(-k, k, (3 * H, H))
+    b_ih, b_hh = rng.uniform(-k, k, 3 * H), rng.uniform(-k, k, 3 * H)
+    x, h0 = rng.standard_normal((B, T, I)), rng.standard_normal((B, H))
+    dy, dhn = rng.standard_normal((B, T, H)), rng.standard_normal((B, H))
+    f = gru_oracle.forward(x, h0, w_ih, w_hh, b_ih, b_hh)
+    fp = gru_oracle.forward_rows_parallel(x, h0, w_ih, w_hh, b_ih, b_hh, threads=3)
+    assert np.array_equal(f.y, fp.y) and np.array_equal(f.hn, fp.hn) and np.array_equal(f.cache, fp.cache)
+    b = gru_oracle.backward(x, h0, w_ih, w_hh, f.y, f.cache, dy, dhn)
+    bp = gru_oracle.backward_rows_parallel(x, h0, w_ih, w_hh, f.y, f.cache, dy, dhn, threads=3)
+    assert np.array_equal(b.dx, bp.dx) and np.array_equal(b.dh0, bp.dh0)
+    for name in ("dw_ih", "dw_hh", "db_ih", "db_hh"):
+        np.testing.assert_allclose(getattr(bp, name), getattr(b, name), rtol=1e-13, atol=1e-13)
