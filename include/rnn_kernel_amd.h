@@ -47,10 +47,12 @@ const char* rka_last_error(void);
  * (src/rnn_kernel/a100/prod/gru.py:109-117,139-148). */
 int rka_device_supported(int device);
 
-/* Bytes of the per-layer gate cache ("reserve": r, z, n, a_n per unit and
- * step) that rka_gru_forward writes in training mode and rka_gru_backward
- * reads.  Replaces the reference's gate_cache [B,T,4H] allocation
- * (src/rnn_kernel/a100/prod/gru.py:238). */
+/* Bytes of the per-layer gate cache ("reserve") that rka_gru_forward writes
+ * in training mode and rka_gru_backward reads: [B,T,H,4] fp32, the unit's
+ * (r, z, n, a_n) contiguous (one 16-byte access per unit and step).
+ * Replaces the reference's gate_cache [B,T,4H] allocation
+ * (src/rnn_kernel/a100/prod/gru.py:238), which keeps the four gates in
+ * blocks of H; the size is the same. */
 size_t rka_gru_reserve_bytes(int batch, int seq_len, int hidden_size);
 
 /* Workspace bytes rka_gru_forward needs (input-gate buffer, exchange

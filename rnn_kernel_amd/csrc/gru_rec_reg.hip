@@ -37,7 +37,7 @@
 //
 // Forward maths (src/rnn_kernel/a100/prod/kernels/a100_gru_h256_kernels.cu:756-776):
 //   a = W_hh h_{t-1} + b_hh; r = sigmoid(gx_r + a_r); z = sigmoid(gx_z + a_z);
-//   n = tanh(gx_n + r a_n); h_t = n + z (h_{t-1} - n); reserve = (r, z, n, a_n)
+//   n = tanh(gx_n + r a_n); h_t = n + z (h_{t-1} - n); reserve[b, t, u] = (r, z, n, a_n)
 // Backward maths (a100_gru_h256_kernels.cu:842-866,915-932), g = dh_t + dy_t:
 //   dz = g (h_{t-1} - n), dn^ = g (1 - z)(1 - n^2), dr^ = dn^ a_n r (1 - r),
 //   dz^ = dz z (1 - z), da_n = dn^ r; dh_{t-1} = g z + G_h W_hh;
@@ -86,19 +86,33 @@ struct RegParams {
 // wave-private LDS row first.  Measured on MI355X, a VGPR-operand v_fmac_f32
 // issues at ~1.2 ns per SIMD with two waves per SIMD against ~2.0 ns for
 // the row-broadcast DPP form and ~2.1 ns with an SGPR operand.
-template <int S, int R>
-__global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
+//
+// IO (one row per workgroup): a ninth wavefront, which never polls, stores
+// the outputs of each step from LDS, so the owner's per-step stores no
+// longer sit in its vector-memory counter ahead of its next poll (the
+// counter retires in issue order).  Same-box A/B at c2: 0.466 vs 0.488 ms
+// per launch.  The owner still loads the input gates one step ahead, after
+// its poll: loads that miss to HBM delay the return of every later load of
+// the CU, the polls of all wavefronts included, so moving them to the I/O
+// wavefront (registers or LDS-DMA, one to three steps ahead) measured 0.53
+// to 0.57 ms, while the same copies from L2-resident addresses measured
+// 0.455 ms.
+template <int S, int R, bool IO>
+__global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
     const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
     const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
     float* __restrict__ reserve, unsigned long long* __restrict__ exch, int* __restrict__ abort_flag,
     RegParams p) {
     static_assert(R == 1 || R == 2 || R == 4, "rows per workgroup");
+    static_assert(!IO || R == 1, "the I/O wavefront serves one row");
     constexpr int NR = S - 1;              // remote slots
     constexpr int NP = NR > 0 ? 8 * NR : 4;  // polled h values per wave half and row
     __shared__ float part[2][4][3][R][64];  // [step parity][k quarter][gate][row][unit]
     __shared__ __attribute__((aligned(16))) float hloc[2][R][64];
     __shared__ __attribute__((aligned(16))) float hrem[NW][R][2][NP];  // per wave, row and half: the polled h values
+    __shared__ float io_out[IO ? 2 : 1][5][64];  // IO: outputs (h, r, z, n, a_n) of a step, by step parity
     __shared__ int s_abort;
+    __shared__ int s_local;
 
     const int B = p.B, T = p.T, H = p.H;
     const int lane = threadIdx.x & 63;
@@ -117,6 +131,56 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     const bool ufvalid = uf < H;
     auto kofh = [&](int half, int j, int i) { return 64 * ((s + j) % S) + 16 * Q + 8 * half + i; };
     auto kof = [&](int j, int i) { return kofh(hf, j, i); };
+
+    if constexpr (IO) {
+        if (wave == NW) {
+            // The I/O wavefront: lane l is unit u of row row0.  Per step t,
+            // before the step's first barrier, it stores the outputs of step
+            // t-1 (written to io_out by the owner before the second barrier
+            // of step t-1).  It takes both barriers of every step and leaves
+            // the loop when the compute wavefronts do.
+            if (threadIdx.x == NW * 64) s_abort = 0;
+            const bool valid = uvalid && row0 < B;
+            float* yp = y + (size_t)row0 * T * H + u;
+            float* rp = reserve ? reserve + (size_t)row0 * T * 4 * H + 4 * u : nullptr;
+            auto store_step = [&](int t, const float (&o)[5]) {
+                if (!valid) return;
+                yp[(size_t)t * H] = o[0];
+                if (rp) *reinterpret_cast<float4*>(rp + (size_t)t * 4 * H) = make_float4(o[1], o[2], o[3], o[4]);
+            };
+            auto read_out = [&](int t, float (&o)[5]) {
+#pragma unroll
+                for (int c = 0; c < 5; ++c) o[c] = io_out[t & 1][c][lane];
+            };
+            const rec::WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
+            (void)rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
+            int t_stop = T;
+            for (int t = 0; t < T; ++t) {
+                if (t >= 1) {
+                    float o[5];
+                    read_out(t - 1, o);
+                    store_step(t - 1, o);
+                }
+                __syncthreads();
+                const bool abort_now = s_abort != 0;
+                __syncthreads();
+                if (abort_now) {
+                    t_stop = t;
+                    break;
+                }
+            }
+            if (t_stop == T) {
+                float o[5];
+                read_out(T - 1, o);
+                store_step(T - 1, o);
+            } else {
+                const float nan = __builtin_nanf("");
+                const float o[5] = {nan, nan, nan, nan, nan};
+                for (int t = t_stop; t < T; ++t) store_step(t, o);
+            }
+            return;
+        }
+    }
 
     // slot j's W_hh entries in w?[8 j .. 8 j + 7]
     float wr[8 * S], wz[8 * S], wn[8 * S];
@@ -174,9 +238,8 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
         bias_n = b_hh[2 * H + u];
         load_gx(gxs[0], 0);
     }
-    if (threadIdx.x == 0) s_abort = 0;
+    if (!IO && threadIdx.x == 0) s_abort = 0;
     const rec::WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
-    __shared__ int s_local;
     const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
 
     // Lane l < 2 NP polls half l / NP, slot 1 + (l % NP) / 8, entry l % 8 of
@@ -209,16 +272,10 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     // outputs of the previous step, stored after the next poll
     float o_h = 0.f, o_r = 0.f, o_z = 0.f, o_n = 0.f, o_a = 0.f;
     float* y_row = y + (size_t)orow * T * H + u;
-    float* res_row = reserve ? reserve + (size_t)orow * T * 4 * H + u : nullptr;
+    float* res_row = reserve ? reserve + (size_t)orow * T * 4 * H + 4 * u : nullptr;
     auto store_outputs = [&](int t) {
         y_row[(size_t)t * H] = o_h;
-        if (res_row) {
-            float* cp = res_row + (size_t)t * 4 * H;
-            cp[0] = o_r;
-            cp[H] = o_z;
-            cp[2 * H] = o_n;
-            cp[3 * H] = o_a;
-        }
+        if (res_row) *reinterpret_cast<float4*>(res_row + (size_t)t * 4 * H) = make_float4(o_r, o_z, o_n, o_a);
     };
     // partial sums of the step in flight per row; the own slot's FMAs land
     // first.  Two accumulators per gate and row give each wave six
@@ -315,7 +372,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
             for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][8 * jj], hv0[jj]);
         }
         if (owner) {
-            if (t > 0) store_outputs(t - 1);
+            if (!IO && t > 0) store_outputs(t - 1);
             if (t + 1 < T) load_gx(nxt, t + 1);
         }
         // @probe:polled
@@ -395,6 +452,13 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
             o_n = n;
             o_a = sn;
             h_prev = h;
+            if constexpr (IO) {
+                io_out[t & 1][0][lane] = h;
+                io_out[t & 1][1][lane] = r;
+                io_out[t & 1][2][lane] = z;
+                io_out[t & 1][3][lane] = n;
+                io_out[t & 1][4][lane] = sn;
+            }
         }
         if (wave < R) hloc[t & 1][wave][lane] = owner ? h_prev : 0.f;  // zero past H and B
         __syncthreads();
@@ -428,11 +492,13 @@ __global__ __launch_bounds__(NTH) void gru_fwd_local_kernel(
     // @probe:kernel_end
     const bool aborted = t_stop < T;
     if (owner) {
-        if (!aborted) {
-            store_outputs(T - 1);
-        } else {
-            o_h = o_r = o_z = o_n = o_a = __builtin_nanf("");
-            for (int t = t_stop; t < T; ++t) store_outputs(t);
+        if constexpr (!IO) {
+            if (!aborted) {
+                store_outputs(T - 1);
+            } else {
+                o_h = o_r = o_z = o_n = o_a = __builtin_nanf("");
+                for (int t = t_stop; t < T; ++t) store_outputs(t);
+            }
         }
         hn[(size_t)orow * H + u] = aborted ? __builtin_nanf("") : h_prev;
     }
@@ -477,6 +543,10 @@ __device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
 // runs the next step's pointwise math, publishes its G words and writes
 // them to LDS; after a second barrier every wave runs the own entries' FMAs
 // while the other slices' words travel.
+//
+// The owner keeps its per-step G stores: the ninth-wavefront form of the
+// forward, with the own entries' weights in LDS to fit 168 VGPRs, measured
+// 0.50-0.51 vs 0.48 ms per c2 launch.
 template <int S, int R>
 __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
@@ -492,6 +562,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     __shared__ __attribute__((aligned(16))) float gloc[R][32][8];      // own G words by j-group (6 used)
     __shared__ __attribute__((aligned(16))) float grem[NW][R][4][GR];  // per wave and row: polled words by j-group
     __shared__ int s_abort;
+    __shared__ int s_local;
 
     const int B = p.B, T = p.T, H = p.H;
     const int H3 = 3 * H;
@@ -502,6 +573,8 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     const int s = gc.s;
     const int u = s * 64 + lane;  // the owner lane's unit
     const bool uvalid = u < H;
+    const int i0 = T - p.t_end, i1 = T - p.t_begin;  // steps i0 .. i1-1 (t = T-1-i)
+
     const int rho = lane >> 4, q = lane & 15;
     const int J = 4 * wave + rho;
     const int ub = s * 64 + 4 * q;  // the lane's first FMA unit
@@ -561,18 +634,18 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         // row pointers are wave-uniform (scalar); the unit is the lane offset
         const size_t bt = (size_t)orow * T + t;
         d[0] = dy ? (dy + bt * H)[u] : 0.f;
-        const float* cp = reserve + bt * 4 * H;
-        d[1] = cp[u];
-        d[2] = cp[H + u];
-        d[3] = cp[2 * H + u];
-        d[4] = cp[3 * H + u];
+        // the unit's (r, z, n, a_n) as one float4 (reserve [B, T, H, 4])
+        const float4 c4 = *reinterpret_cast<const float4*>(reserve + bt * 4 * H + 4 * u);
+        d[1] = c4.x;
+        d[2] = c4.y;
+        d[3] = c4.z;
+        d[4] = c4.w;
         d[5] = t > 0 ? (y + (bt - 1) * H)[u] : (h0 + (size_t)orow * H)[u];
     };
 #pragma unroll
     for (int e = 0; e < 2; ++e)
 #pragma unroll
         for (int c = 0; c < 6; ++c) ins[e][c] = 0.f;
-    const int i0 = T - p.t_end, i1 = T - p.t_begin;
     if (owner) {
         if (dhn) dh = dhn[(size_t)orow * H + u];
         load_inputs(ins[0], T - 1 - i0);
@@ -580,7 +653,6 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     }
     if (threadIdx.x == 0) s_abort = 0;
     const rec::WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
-    __shared__ int s_local;
     const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
 
     // Wave w polls remote entries WE w .. WE w + WE - 1 of every row:
@@ -802,7 +874,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
 
 // ------------------------------------------------------------- config ---
 template <int S>
-const void* local_ptr(int dir, int rows) {
+const void* local_ptr(int dir, int rows, bool io) {
     if (dir == 1) {
         switch (rows) {
             case 1: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 1>);
@@ -811,20 +883,29 @@ const void* local_ptr(int dir, int rows) {
         }
     }
     switch (rows) {
-        case 1: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1>);
-        case 2: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 2>);
-        default: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 4>);
+        case 1:
+            return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true>)
+                      : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false>);
+        case 2: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 2, false>);
+        default: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 4, false>);
     }
 }
+
+// Whether the kernel for (dir, rows) has the I/O wavefront: the forward
+// with one row per workgroup.
+bool uses_io(int dir, int rows) { return dir == 0 && rows == 1; }
+
+int block_threads(int dir, int rows) { return uses_io(dir, rows) ? NTH + 64 : NTH; }
 
 // The local-slice kernels: S slices, 1, 2 or 4 batch rows per workgroup.
 const void* kernel_ptr(int dir, int cap, int rows, int slices) {
     (void)cap;
+    const bool io = uses_io(dir, rows);
     switch (slices) {
-        case 1: return local_ptr<1>(dir, rows);
-        case 2: return local_ptr<2>(dir, rows);
-        case 3: return local_ptr<3>(dir, rows);
-        default: return local_ptr<4>(dir, rows);
+        case 1: return local_ptr<1>(dir, rows, io);
+        case 2: return local_ptr<2>(dir, rows, io);
+        case 3: return local_ptr<3>(dir, rows, io);
+        default: return local_ptr<4>(dir, rows, io);
     }
 }
 
@@ -865,7 +946,8 @@ int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_
         if (rows > max_rows(dir, S) || (fixed_rows && rows != fixed_rows)) continue;
         const int G = (batch + rows - 1) / rows;
         int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows, S), NTH, 0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows, S), block_threads(dir, rows),
+                                                         0) != hipSuccess)
             continue;
         const long resident = (long)per_cu * dev.num_cus;
         chosen = rows;  // the last candidate (the most rows) unless one fits
@@ -901,12 +983,14 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                         (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
+        RKA_RETURN_IF_HIP(
+            hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(block_threads(dir, c.rows)), args, 0, stream));
     } else {
         void* args[] = {(void*)&a.dy, (void*)&a.dhn, (void*)&a.reserve, (void*)&a.h0, (void*)&a.y,
                         (void*)&a.w_hh, (void*)&a.gout, (void*)&a.dh0, (void*)&a.exch, (void*)&a.abort_flag,
                         (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, 0, stream));
+        RKA_RETURN_IF_HIP(
+            hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(block_threads(dir, c.rows)), args, 0, stream));
     }
     return 0;
 }

@@ -12,7 +12,7 @@
 //
 // Forward maths (src/rnn_kernel/a100/prod/kernels/a100_gru_h256_kernels.cu:756-776):
 //   a = W_hh h_{t-1} + b_hh; r = sigmoid(gx_r + a_r); z = sigmoid(gx_z + a_z);
-//   n = tanh(gx_n + r a_n); h_t = n + z (h_{t-1} - n); reserve = (r, z, n, a_n)
+//   n = tanh(gx_n + r a_n); h_t = n + z (h_{t-1} - n); reserve[b, t, u] = (r, z, n, a_n)
 // Backward maths (a100_gru_h256_kernels.cu:842-866,915-932), g = dh_t + dy_t:
 //   dz = g (h_{t-1} - n), dn^ = g (1 - z)(1 - n^2), dr^ = dn^ a_n r (1 - r),
 //   dz^ = dz z (1 - z), da_n = dn^ r; dh_{t-1} = g z + G_h W_hh.
@@ -206,13 +206,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
                          pack_word(h, (unsigned)(t + 1)), xlocal);
             const size_t bt = (size_t)b * T + t;
             y[bt * H + u] = h;
-            if (reserve) {
-                float* cp = reserve + bt * 4 * H;
-                cp[u] = r;
-                cp[H + u] = z;
-                cp[2 * H + u] = n;
-                cp[3 * H + u] = sn;
-            }
+            if (reserve) *reinterpret_cast<float4*>(reserve + bt * 4 * H + 4 * u) = make_float4(r, z, n, sn);
             h_prev = h;
             if (t + 1 < T) {
                 const float* gp = gx + (bt + 1) * 3 * H;
@@ -228,13 +222,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
         for (int t = t_stop; t < T; ++t) {
             const size_t bt = (size_t)b * T + t;
             y[bt * H + u] = nan;
-            if (reserve) {
-                float* cp = reserve + bt * 4 * H;
-                cp[u] = nan;
-                cp[H + u] = nan;
-                cp[2 * H + u] = nan;
-                cp[3 * H + u] = nan;
-            }
+            if (reserve) *reinterpret_cast<float4*>(reserve + bt * 4 * H + 4 * u) = make_float4(nan, nan, nan, nan);
         }
         hn[(size_t)b * H + u] = aborted ? nan : h_prev;
     }
@@ -293,8 +281,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
         const int tl = p.t_end - 1;
         const size_t bt = (size_t)b * T + tl;
         if (dy) dyv = dy[bt * H + u];
-        const float* cp = reserve + bt * 4 * H;
-        cr = cp[u]; cz = cp[H + u]; cn = cp[2 * H + u]; ca = cp[3 * H + u];
+        const float4 c4 = *reinterpret_cast<const float4*>(reserve + bt * 4 * H + 4 * u);
+        cr = c4.x; cz = c4.y; cn = c4.z; ca = c4.w;
         hp = (tl > 0) ? y[(bt - 1) * H + u] : h0[(size_t)b * H + u];
     }
     const int kbeg = kc * p.KCH;
@@ -339,8 +327,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
             if (t > p.t_begin) {
                 const size_t pbt = bt - 1;
                 dyv = dy ? dy[pbt * H + u] : 0.f;
-                const float* cp = reserve + pbt * 4 * H;
-                cr = cp[u]; cz = cp[H + u]; cn = cp[2 * H + u]; ca = cp[3 * H + u];
+                const float4 c4 = *reinterpret_cast<const float4*>(reserve + pbt * 4 * H + 4 * u);
+                cr = c4.x; cz = c4.y; cn = c4.z; ca = c4.w;
                 hp = (t > 1) ? y[(pbt - 1) * H + u] : h0[(size_t)b * H + u];
             }
         }
