@@ -14,10 +14,11 @@
 // ds_read_b128 feeding four MFMAs: a k-major tile is kept [k][row] (a lane
 // reads four rows at one k), a row-major one [row][k] (four k of one row;
 // swizzled in the ring, padded in the register path), and a lane's four B
-// blocks are four adjacent output columns, stored as one float4.  At c2:
-// input projection 124 us, dx 111 us, dW 135/130 us (the register-staged
-// loop alone: 128, 121, 143/133 us).  Each operand layout is a template instance, so no product carries
-// another's address arithmetic.  The weight gradients (K = B*T rows) use
+// blocks are four adjacent output columns, stored as one float4 (a
+// streaming store for the direct products).  At c2 inside the training
+// step: input projection 121 us, dx 110 us, the dW pair 243 us.  Each
+// operand layout is a template instance, so no product carries another's
+// address arithmetic.  The weight gradients (K = B*T rows) use
 // split-K with a fixed-order reduction, so results are deterministic run to
 // run.
 #include "rka_internal.h"
@@ -176,7 +177,7 @@ struct GemmArgs {
     int c_vec;             // float4 stores of C / partials allowed
     float* partial;        // split mode: [ksplit][m][n] then colsum [ksplit][m]
     int want_colsum;
-    int tiles_m, tiles;    // split mode: output tiles along m, in total
+    int tiles_m, tiles;    // output tiles along m, in total
     int ksplit;            // split mode: slices of this launch
     int z_off, ksplit_total;  // split mode: first slice, slices in the buffer
     SegMap c_seg;          // direct mode: output row map
@@ -199,6 +200,24 @@ __device__ __forceinline__ void split_coords(const GemmArgs& p, int id, int& bx,
     }
     bx = tile % p.tiles_m;
     by = tile / p.tiles_m;
+}
+
+// Direct mode runs a 1-D grid of tiles.  When the row panels divide among
+// the 8 XCDs (workgroup id % 8), the N-tiles of one row panel get
+// consecutive ids on one XCD, so the panel's A rows are fetched from HBM
+// once and re-read from that XCD's L2 by the panel's other tiles (at c2 the
+// input projection's 1536 tiles run as two resident waves, and in row-panel
+// order each X panel was fetched once per wave).
+__device__ __forceinline__ void direct_coords(const GemmArgs& p, int id, int& bx, int& by) {
+    const int tn = p.tiles / p.tiles_m;
+    if (p.tiles_m % 8 == 0) {
+        const int q = id / 8;
+        bx = id % 8 + 8 * (q / tn);
+        by = q % tn;
+        return;
+    }
+    bx = id % p.tiles_m;
+    by = id / p.tiles_m;
 }
 
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l%16][k = l/16] and
@@ -346,7 +365,9 @@ constexpr int kDmaTile = 16 * BM;  // floats per operand tile
 //     the rotated column: t = 64 (n/64) + 16 (n%4) + (n%64)/4), k quad
 //     (s%4) ^ ((t/4)%4).  The 16 lanes of one ds_read_b128 (one k quad g,
 //     rows 16a + i of A or columns 4i + b of B) then fall on 16 distinct
-//     4-bank groups.
+//     4-bank groups.  (rocprofv3 counts 4 bank-conflict cycles per such
+//     read; a swizzle that also spreads every 8-lane group over 128 bytes
+//     left that count and the run time unchanged.)
 template <int KMAJOR, bool SHIFT, bool SEG, bool ROT>
 __device__ __forceinline__ const float* dma_src(const GemmOperand& op, int r0, int k0, int s) {
     if constexpr (KMAJOR == 1) {
@@ -472,7 +493,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int
                 dst = p.c + (size_t)seg_map<SEG>(p.c_seg, m) * p.ldc + n;
             }
             if (vec_store) {
-                *reinterpret_cast<float4*>(dst) = v;
+                if (!SPLIT) {
+                    // streaming store: C is written once and not re-read by
+                    // this kernel (the output write costs ~4 us less at c2)
+                    const floatx4 vv = {v.x, v.y, v.z, v.w};
+                    __builtin_nontemporal_store(vv, reinterpret_cast<floatx4*>(dst));
+                } else {
+                    *reinterpret_cast<float4*>(dst) = v;
+                }
             } else {
                 dst[0] = v.x;
                 if (n + 1 < p.n) dst[1] = v.y;
@@ -490,8 +518,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int
 template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<AK, BK>()];
-    int bx = blockIdx.x, by = blockIdx.y, bz = 0;
-    if (SPLIT) split_coords(p, blockIdx.x, bx, by, bz);
+    int bx, by, bz = 0;
+    if (SPLIT)
+        split_coords(p, blockIdx.x, bx, by, bz);
+    else
+        direct_coords(p, blockIdx.x, bx, by);
     gemm_tile<AK, BKM, BSHIFT, SPLIT, SEG, BK>(p, bx, by, bz, smem);
 }
 
@@ -627,7 +658,7 @@ template <bool SPLIT>
 int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream) {
     finish_args<SPLIT>(args, ksplit, av, bv);
     const int tm = args.tiles_m, tn = args.tiles / args.tiles_m;
-    const dim3 grid = SPLIT ? dim3(tm * tn * ksplit) : dim3(tm, tn);
+    const dim3 grid(SPLIT ? tm * tn * ksplit : tm * tn);
     const bool seg = args.a.seg.len || args.b.seg.len || args.c_seg.len;
     return seg ? launch_gemm_t<SPLIT, true>(args, grid, stream) : launch_gemm_t<SPLIT, false>(args, grid, stream);
 }
@@ -638,7 +669,7 @@ int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
                 const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg) {
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
     if (!a.ptr || !b.ptr || !c) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: null operand");
-    if (m > 65535 * BM || n > 65535 * BN) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
+    if ((long long)((m + BM - 1) / BM) * ((n + BN - 1) / BN) > 0x7fffffff) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
     GemmArgs args{};
     args.a = a;
     args.b = b;
