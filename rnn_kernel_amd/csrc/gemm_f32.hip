@@ -181,6 +181,8 @@ struct GemmArgs {
     int ksplit;            // split mode: slices of this launch
     int z_off, ksplit_total;  // split mode: first slice, slices in the buffer
     SegMap c_seg;          // direct mode: output row map
+    unsigned long long* zero;  // direct mode: words cleared on the side (nullable)
+    size_t zero_words;
 };
 
 // Split mode runs a 1-D grid of tiles * ksplit workgroups.  Workgroups are
@@ -519,10 +521,13 @@ template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? k
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<AK, BK>()];
     int bx, by, bz = 0;
-    if (SPLIT)
+    if (SPLIT) {
         split_coords(p, blockIdx.x, bx, by, bz);
-    else
+    } else {
         direct_coords(p, blockIdx.x, bx, by);
+        for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < p.zero_words; i += (size_t)gridDim.x * NT)
+            p.zero[i] = 0ull;
+    }
     gemm_tile<AK, BKM, BSHIFT, SPLIT, SEG, BK>(p, bx, by, bz, smem);
 }
 
@@ -666,7 +671,8 @@ int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream)
 }  // namespace
 
 int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
-                const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg) {
+                const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg,
+                unsigned long long* zero, size_t zero_words) {
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
     if (!a.ptr || !b.ptr || !c) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: null operand");
     if ((long long)((m + BM - 1) / BM) * ((n + BN - 1) / BN) > 0x7fffffff) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
@@ -682,6 +688,8 @@ int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
     args.ldc = ldc;
     args.c_vec = (ldc % 4 == 0 && aligned16(c)) ? 1 : 0;
     args.c_seg = c_seg;
+    args.zero = zero;
+    args.zero_words = zero ? zero_words : 0;
     return launch_gemm<false>(args, 1, vec_ok(a, m, k), vec_ok(b, n, k), stream);
 }
 

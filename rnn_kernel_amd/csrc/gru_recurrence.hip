@@ -292,7 +292,7 @@ int launch_rec_forward_noalloc(const float* gx, const float* h0, const float* w_
 
 int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
                        float* y, float* hn, float* reserve, void* ws, size_t ws_bytes,
-                       int B, int T, int H, hipStream_t stream) {
+                       int B, int T, int H, hipStream_t stream, bool zero_ws) {
     rec::Args a;
     a.gx = gx;
     a.h0 = h0;
@@ -306,7 +306,7 @@ int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, cons
     a.H = H;
     a.t_begin = 0;
     a.t_end = T;
-    return launch(0, a, ws, ws_bytes, true, stream);
+    return launch(0, a, ws, ws_bytes, zero_ws, stream);
 }
 
 int launch_rec_backward(const float* dy, const float* dhn, const float* reserve,

@@ -316,12 +316,17 @@ int rka_gru_forward(const float* x, const float* h0, const float* w_ih, const fl
     // Gx = X W_ih^T + b_ih  (both operands row-major, k = input feature)
     GemmOperand a{x, I, 0, 0, nullptr};
     GemmOperand b{w_ih, I, 0, 0, nullptr};
+    // the GEMM also clears the recurrence's exchange state (slots, start-up
+    // XCD words, abort flag), which saves the recurrence its fill launch
+    unsigned long long* rec_state = reinterpret_cast<unsigned long long*>(ws + l.rec);
+    const size_t rec_words = rec_workspace_bytes(B, H) / sizeof(unsigned long long);
     {
         StageScope scope(0, s);
-        RKA_RETURN_IF_ERR(gemm_direct(B * T, 3 * H, I, a, b, b_ih, gx, 3 * H, s));
+        RKA_RETURN_IF_ERR(gemm_direct(B * T, 3 * H, I, a, b, b_ih, gx, 3 * H, s, SegMap{}, rec_state, rec_words));
     }
     StageScope scope(1, s);
-    return launch_rec_forward(gx, h0, w_hh, b_hh, y, hn, reserve, ws + l.rec, l.total - l.rec, B, T, H, s);
+    return launch_rec_forward(gx, h0, w_hh, b_hh, y, hn, reserve, ws + l.rec, l.total - l.rec, B, T, H, s,
+                              false);
 }
 
 int rka_gru_backward(const float* x, const float* h0, const float* w_ih, const float* w_hh,

@@ -71,8 +71,11 @@ struct GemmOperand {
 
 // C[m,n] = sum_k A(m,k) B(n,k) + bias[n]; direct store (row m of C at
 // c_seg(m)).
+// zero / zero_words: a buffer of 64-bit words the launch also clears (the
+// next kernel's exchange state, so that it needs no fill launch of its own).
 int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
-                const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg = SegMap{});
+                const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg = SegMap{},
+                unsigned long long* zero = nullptr, size_t zero_words = 0);
 
 // Split-K partial products only: slices [z_off, z_off + ksplit) of a
 // partial buffer holding ksplit_total slices (layout as gemm_splitk).
@@ -149,9 +152,11 @@ int rec_abort_count(unsigned long long* count);
 size_t rec_workspace_bytes(int batch, int hidden);
 int eval_gate_functions(const float* x, float* sig, float* th, int n, hipStream_t stream);
 
+// zero_ws false: the workspace's recurrence state was cleared by an earlier
+// kernel on the stream (rka_gru_forward's input GEMM).
 int launch_rec_forward(const float* gx, const float* h0, const float* w_hh, const float* b_hh,
                        float* y, float* hn, float* reserve, void* ws, size_t ws_bytes,
-                       int B, int T, int H, hipStream_t stream);
+                       int B, int T, int H, hipStream_t stream, bool zero_ws = true);
 // The same with the exchange state in a static per-device array (no
 // workspace); 2 B H words at most rec_noalloc_max_slot_bytes() / 8.
 int launch_rec_forward_noalloc(const float* gx, const float* h0, const float* w_hh, const float* b_hh, float* y,

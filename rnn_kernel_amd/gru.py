@@ -320,9 +320,17 @@ class GRU(nn.Module):
         return hx
 
     def _run(self, x: torch.Tensor, hx: torch.Tensor, layer_fn):
+        # Per-layer initial states as views whose backward needs no kernel
+        # for one layer (a reshape of the gradient) and one stack for
+        # several; hx[layer] would zero-fill a [L, B, H] gradient and copy
+        # into it for every layer.
+        if self.num_layers == 1:
+            h_layers = (hx.reshape(hx.shape[1:]),)
+        else:
+            h_layers = hx.unbind(0)
         layer_input, h_list = x, []
         for layer in range(self.num_layers):
-            layer_input, h_layer = layer_fn(layer_input, hx[layer], *self._layer_parameters(layer))
+            layer_input, h_layer = layer_fn(layer_input, h_layers[layer], *self._layer_parameters(layer))
             h_list.append(h_layer)
         h_n = h_list[0] if len(h_list) == 1 else torch.cat(h_list, dim=0)
         return layer_input, h_n

@@ -33,7 +33,10 @@ def _no_tf32():
 
 
 # ------------------------------------------------------------------ GEMM ---
-GEMM_SHAPES = [(128, 128, 16), (300, 200, 50), (1, 1, 1), (4096, 768, 256), (129, 387, 130), (768, 256, 4096)]
+# (1000, 390, 70): eight row panels, so the XCD-aware tile order, with edge
+# tiles along both m and n and a k that is not a multiple of 16
+GEMM_SHAPES = [(128, 128, 16), (300, 200, 50), (1, 1, 1), (4096, 768, 256), (129, 387, 130), (768, 256, 4096),
+               (1000, 390, 70)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
