@@ -319,11 +319,11 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
             publish_word(wp + H, pack_word(dzh, tag), xlocal);
             publish_word(wp + 2 * H, pack_word(dan, tag), xlocal);
             const size_t bt = (size_t)b * T + t;
-            float* op = gout + bt * 4 * H;
-            op[u] = dan;
-            op[H + u] = drh;
-            op[2 * H + u] = dzh;
-            op[3 * H + u] = dnh;
+            float* op = gout + bt * 4 * H;  // streaming stores, as in the register family
+            __builtin_nontemporal_store(dan, op + u);
+            __builtin_nontemporal_store(drh, op + H + u);
+            __builtin_nontemporal_store(dzh, op + 2 * H + u);
+            __builtin_nontemporal_store(dnh, op + 3 * H + u);
             if (t > p.t_begin) {
                 const size_t pbt = bt - 1;
                 dyv = dy ? dy[pbt * H + u] : 0.f;
