@@ -188,7 +188,7 @@ def _run_forward(x, h0, weight_ih, weight_hh, bias_ih, bias_hh, training: bool):
     h_n = torch.empty(1, batch, hidden, device=device, dtype=torch.float32)
     reserve = None
     if training:
-        reserve = torch.empty(batch, seq_len, 4 * hidden, device=device, dtype=torch.float32)
+        reserve = torch.empty(batch, seq_len, hidden, 4, device=device, dtype=torch.float32)  # (r, z, n, a_n) per unit
     ws_bytes = lib.rka_gru_forward_workspace_bytes(batch, seq_len, input_size, hidden)
     with torch.cuda.device(index):
         ws = _workspace(ws_bytes, device)
