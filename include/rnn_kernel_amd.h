@@ -166,6 +166,19 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
  *         0 = auto);
  * kind 2: register-resident; units = 64 (or 0), param = batch rows per
  *         workgroup (1, 2, 4, 0 = auto). */
+/* GEMM tile families (for tuning and A/B tests; affects later calls on all
+ * threads).  RKA_GEMM_TILES_AUTO: the weight-gradient pair of
+ * rka_gru_backward runs in 192x256 tiles, one twelve-wavefront workgroup
+ * per CU, when its tiles and k-slices divide evenly over the CUs (c2, c4);
+ * every other product in 128x128 tiles.  RKA_GEMM_TILES_128: 128x128 tiles
+ * everywhere.  The results are the same bit for bit (each output element
+ * sums its k in the same order, over the same k-slices).  No counterpart in
+ * the reference (its products are cuBLAS calls,
+ * src/rnn_kernel/a100/prod/gru.py:569-578). */
+#define RKA_GEMM_TILES_AUTO 0
+#define RKA_GEMM_TILES_128 1
+int rka_set_gemm_tiles(int mode);
+
 /* Number of time chunks the backward of a layer runs in (0 = automatic,
  * currently 1; at most 8, and never more than seq_len).  With several chunks
  * the backward recurrence is launched once per time range, latest first,

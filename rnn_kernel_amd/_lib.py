@@ -36,6 +36,7 @@ SIGNATURES = {
     "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
     "rka_set_backward_chunks": (_I, [_I]),
     "rka_set_spin_limit": (_I, [_I]),
+    "rka_set_gemm_tiles": (_I, [_I]),
     "rka_recurrence_abort_count": (_I, [ctypes.POINTER(ctypes.c_ulonglong)]),
     "rka_set_stall_block": (_I, [_I]),
     "rka_backward_chunks": (_I, [_I]),
@@ -142,6 +143,12 @@ def set_spin_limit(polls: int) -> None:
     """Poll rounds a recurrence wait makes before it gives up (0 = the
     default, 2^24); see rka_set_spin_limit."""
     check(load().rka_set_spin_limit(polls), "rka_set_spin_limit")
+
+
+def set_gemm_tiles(mode: int) -> None:
+    """GEMM tile families: 0 = automatic (large persistent tiles where they
+    divide evenly), 1 = 128x128 everywhere; see rka_set_gemm_tiles."""
+    check(load().rka_set_gemm_tiles(mode), "rka_set_gemm_tiles")
 
 
 def set_stall_block(block: int) -> None:

@@ -21,6 +21,8 @@
 // address arithmetic.  The weight gradients (K = B*T rows) use
 // split-K with a fixed-order reduction, so results are deterministic run to
 // run.
+#include <atomic>
+
 #include "rka_internal.h"
 
 namespace rka {
@@ -370,10 +372,11 @@ constexpr int kDmaTile = 16 * BM;  // floats per operand tile
 //     4-bank groups.  (rocprofv3 counts 4 bank-conflict cycles per such
 //     read; a swizzle that also spreads every 8-lane group over 128 bytes
 //     left that count and the run time unchanged.)
-template <int KMAJOR, bool SHIFT, bool SEG, bool ROT>
+// R: rows of the tile (k form: R / 4 chunks per k row).
+template <int KMAJOR, bool SHIFT, bool SEG, bool ROT, int R = BM>
 __device__ __forceinline__ const float* dma_src(const GemmOperand& op, int r0, int k0, int s) {
     if constexpr (KMAJOR == 1) {
-        return elem_ptr<1, SHIFT, SEG>(op, r0 + 4 * (s & 31), k0 + (s >> 5));
+        return elem_ptr<1, SHIFT, SEG>(op, r0 + 4 * (s % (R / 4)), k0 + s / (R / 4));
     } else {
         const int t = s >> 2;
         const int kq = (s & 3) ^ ((t >> 2) & 3);
@@ -426,43 +429,12 @@ constexpr int gemm_smem_floats() {
     return BK == 16 && kDmaStages * 2 * kDmaTile > 2 * AF + 2 * BF ? kDmaStages * 2 * kDmaTile : 2 * AF + 2 * BF;
 }
 
-// One output tile (bx, by) of k-chunk bz.
-template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int bz, float* smem) {
-    constexpr int AF = lds_tile_floats<AK, BK>();
-    constexpr int BF = lds_tile_floats<1, BK>();
-    constexpr bool kDma = BK == 16;
-    float* As0 = smem;
-    float* As1 = smem + AF;
-    float* Bs0 = smem + 2 * AF;
-    float* Bs1 = smem + 2 * AF + BF;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
-    const int m0 = bx * BM;
-    const int n0 = by * BN;
-    const int kbeg = bz * p.kchunk;
-    const int kend = min(p.k, kbeg + p.kchunk);
-    const int nkb = (kend - kbeg + BK - 1) / BK;
-    const bool colsum = SPLIT && p.want_colsum && by == 0;
-
-    floatx4 acc[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float cs = 0.f;
-
-    if (kDma && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 && (kend - kbeg) % BK == 0)
-        mainloop_dma<AK, BKM, BSHIFT, SEG>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, smem, acc);
-    else
-        mainloop<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
-                                           Bs1, acc);
-
-    // Epilogue: acc[a][b][r] is C(row(a, 4 g + r), n0 + 64 wn + 4 c + b); a
-    // lane's four b values are one float4 of a C row.
+// Epilogue of one output tile: acc[a][b][r] is C(row(a, 4 g + r), n0 + 64 wn
+// + 4 c + b); a lane's four b values are one float4 of a C row (a partial
+// row of slice bz in split mode).
+template <int AK, bool SPLIT, bool SEG>
+__device__ __forceinline__ void store_c(const GemmArgs& p, int m0, int n0, int bz, int wm, int wn, int lane,
+                                        const floatx4 (&acc)[4][4]) {
     const int c = lane & 15, g = lane >> 4;
     const int n = n0 + wn * 64 + 4 * c;
     float4 bias4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -511,6 +483,43 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int
             }
         }
     }
+}
+
+// One output tile (bx, by) of k-chunk bz.
+template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int bz, float* smem) {
+    constexpr int AF = lds_tile_floats<AK, BK>();
+    constexpr int BF = lds_tile_floats<1, BK>();
+    constexpr bool kDma = BK == 16;
+    float* As0 = smem;
+    float* As1 = smem + AF;
+    float* Bs0 = smem + 2 * AF;
+    float* Bs1 = smem + 2 * AF + BF;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int m0 = bx * BM;
+    const int n0 = by * BN;
+    const int kbeg = bz * p.kchunk;
+    const int kend = min(p.k, kbeg + p.kchunk);
+    const int nkb = (kend - kbeg + BK - 1) / BK;
+    const bool colsum = SPLIT && p.want_colsum && by == 0;
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float cs = 0.f;
+
+    if (kDma && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 && (kend - kbeg) % BK == 0)
+        mainloop_dma<AK, BKM, BSHIFT, SEG>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, smem, acc);
+    else
+        mainloop<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
+                                           Bs1, acc);
+    store_c<AK, SPLIT, SEG>(p, m0, n0, bz, wm, wn, lane, acc);
     if (colsum && tid < BM && m0 + tid < p.m) {
         float* cpart = p.partial + (size_t)p.ksplit_total * p.m * p.n;
         cpart[(size_t)(p.z_off + bz) * p.m + m0 + tid] = cs;
@@ -548,6 +557,150 @@ __global__ __launch_bounds__(NT) void gemm_f32_pair_kernel(GemmArgs p0, GemmArgs
         split_coords(p1, blockIdx.x - blocks0, bx, by, bz);
         gemm_tile<1, 1, false, true, SEG, kSplitBK>(p1, bx, by, bz, smem);
     }
+}
+
+// ------------------------------------- large-tile weight-gradient pair ---
+// The two split-K weight-gradient products (both operands k-major) with
+// workgroups of WMW x WNW wavefronts, each wavefront computing a 64x64
+// sub-tile exactly as above (the same LDS forms and MFMA order, so every
+// partial sum equals the 128x128 kernel's bit for bit): a workgroup tile is
+// (64 WMW) x (64 WNW), one (tile, k-slice) item per workgroup and one
+// workgroup per CU.  At c2 the 3H = 768 gate rows and the 256 columns of
+// each product are four 192x256 tiles, 32 k-slices each, 256 items in all.
+// A 192x256 tile loads 28 KB of operands per 16-deep stage for 1.57 MFLOP,
+// against 16 KB for 0.52 MFLOP with 128x128 tiles; twelve wavefronts keep
+// three per SIMD, as three 128x128 workgroups per CU do.  The operand tiles
+// go straight to LDS through a ring of BigTile::D stages (five: 140 KB).
+// Measured at c2 (same box, three alternating pairs): 234.5 vs 240.5 us.
+// The same workgroups for the direct products (256x192 tiles for the
+// input projection, 128x256 for the input gradient, one workgroup per CU)
+// measured slower than three 128x128 workgroups per CU: 125 vs 120 us and
+// 126 vs 110 us.
+template <int WMW, int WNW>
+struct BigTile {
+    static constexpr int BM = 64 * WMW, BN = 64 * WNW, NW = WMW * WNW, NT = 64 * NW;
+    static constexpr int ACH = BM / 16, BCH = BN / 16, CH = ACH + BCH;  // 1 KB wave loads per stage
+    static constexpr int STAGE = 16 * (BM + BN);                        // floats per ring stage
+    // ring stages: as many as 160 KB of LDS holds, at most 6
+    static constexpr int D = 163840 / (STAGE * 4) < 6 ? 163840 / (STAGE * 4) : 6;
+    static constexpr int SMEM_BYTES = D * STAGE * 4;
+    static_assert(D >= 3, "the ring needs three stages");
+};
+
+// s_waitcnt vmcnt(n) with expcnt / lgkmcnt left at their maxima (gfx9
+// encoding: vmcnt bits 3:0); n is wave-uniform.  n above 15 waits for
+// everything (never less than asked).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+        case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+        case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+        case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+        case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+        case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+        case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+        case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+        case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+        case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+        case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+        case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+        case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+        case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
+// One item (split_coords(p, id)) of a split-K product of k-major operands.
+template <int WMW, int WNW, bool BSHIFT>
+__device__ __forceinline__ void big_split_item(const GemmArgs& p, int id, float* smem) {
+    using T = BigTile<WMW, WNW>;
+    constexpr int D = T::D;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WMW, wn = wave / WMW;
+    const int nw = (T::CH - wave + T::NW - 1) / T::NW;  // this wave's loads per stage
+    int bx, by, bz;
+    split_coords(p, id, bx, by, bz);
+    const int m0 = bx * T::BM, n0 = by * T::BN, kbeg = bz * p.kchunk;
+    const int nkb = p.kchunk / 16;
+    const bool colsum = p.want_colsum && by == 0;
+    auto issue = [&](int kb) {
+        const int k0 = kbeg + 16 * kb;
+        float* st = smem + (kb % D) * T::STAGE;
+        for (int c = wave; c < T::CH; c += T::NW) {
+            if (c < T::ACH)
+                lds_dma16(dma_src<1, false, false, false, T::BM>(p.a, m0, k0, 64 * c + lane), st + 256 * c);
+            else
+                lds_dma16(dma_src<1, BSHIFT, false, false, T::BN>(p.b, n0, k0, 64 * (c - T::ACH) + lane),
+                          st + 16 * T::BM + 256 * (c - T::ACH));
+        }
+    };
+    for (int kb = 0; kb < D - 1 && kb < nkb; ++kb) issue(kb);
+    const int i = lane & 15, g = lane >> 4;
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float cs = 0.f;
+    for (int kb = 0; kb < nkb; ++kb) {
+        // stage kb has landed once at most the later stages already issued
+        // (up to D - 2 of them, nw loads each) are outstanding
+        wait_vmcnt(nw * min(D - 2, nkb - 1 - kb));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const float* as = smem + (kb % D) * T::STAGE;
+        const float* bs = as + 16 * T::BM;
+        // operand fragments of this stage (the k forms and order of
+        // mma_tile), then the first MFMA step, so the matrix cores start
+        // before the loads into the freed stage are addressed and issued
+        float4 fa[4], fb[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            fa[x] = *reinterpret_cast<const float4*>(as + (4 * g + x) * T::BM + wm * 64 + 4 * i);
+            fb[x] = *reinterpret_cast<const float4*>(bs + (4 * g + x) * T::BN + wn * 64 + 4 * i);
+        }
+        auto mstep = [&](int j) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[j][a], fb[j][b], acc[a][b], 0, 0, 0);
+        };
+        __builtin_amdgcn_sched_barrier(0);
+        mstep(0);
+        __builtin_amdgcn_sched_barrier(0);
+        // the stage consumed at kb - 1 is free: every wave is past its reads
+        if (kb + D - 1 < nkb) issue(kb + D - 1);
+        if (colsum && tid < T::BM) {
+            // column sums of A (the bias gradients), in k order
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) cs += as[kk * T::BM + tid];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mstep(1);
+        mstep(2);
+        mstep(3);
+    }
+    store_c<1, true, false>(p, m0, n0, bz, wm, wn, lane, acc);
+    if (colsum && tid < T::BM) {
+        float* cpart = p.partial + (size_t)p.ksplit_total * p.m * p.n;
+        cpart[(size_t)(p.z_off + bz) * p.m + m0 + tid] = cs;
+    }
+}
+
+// The two weight-gradient products, one item per workgroup: items
+// [0, tiles0 * ksplit0) of the first, then the second's.
+template <int WMW, int WNW, bool SHIFT0>
+__global__ __launch_bounds__(64 * WMW * WNW) void gemm_big_pair_kernel(GemmArgs p0, GemmArgs p1) {
+    extern __shared__ __attribute__((aligned(16))) float big_smem[];
+    const int items0 = p0.tiles * p0.ksplit;
+    if ((int)blockIdx.x < items0)
+        big_split_item<WMW, WNW, SHIFT0>(p0, blockIdx.x, big_smem);
+    else
+        big_split_item<WMW, WNW, false>(p1, blockIdx.x - items0, big_smem);
 }
 
 // out[o*ldc + n] = sum_z partial[z][(o+rot)%m][n]; colsum likewise.  With
@@ -668,7 +821,16 @@ int launch_gemm(GemmArgs args, int ksplit, bool av, bool bv, hipStream_t stream)
     return seg ? launch_gemm_t<SPLIT, true>(args, grid, stream) : launch_gemm_t<SPLIT, false>(args, grid, stream);
 }
 
+std::atomic<int> g_gemm_tiles{RKA_GEMM_TILES_AUTO};
+
 }  // namespace
+
+int set_gemm_tiles(int mode) {
+    if (mode != RKA_GEMM_TILES_AUTO && mode != RKA_GEMM_TILES_128)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "rka_set_gemm_tiles: mode must be 0 or 1");
+    g_gemm_tiles.store(mode);
+    return 0;
+}
 
 int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
                 const float* bias, float* c, int ldc, hipStream_t stream, SegMap c_seg,
@@ -733,6 +895,33 @@ int split_args(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, 
     finish_args<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k));
     return 0;
 }
+
+// The weight-gradient pair in 192x256 tiles (3H = 768 gate rows in four
+// tiles, n = H or I = 256 in one), one item (tile, k-slice) per workgroup.
+// Every k-slice must be whole 16-deep stages of the same length.
+int try_big_pair(GemmArgs a0, GemmArgs a1, bool shift0, hipStream_t stream, bool* launched) {
+    *launched = false;
+    if (g_gemm_tiles.load(std::memory_order_relaxed) != RKA_GEMM_TILES_AUTO) return 0;
+    const DeviceInfo* dev = nullptr;
+    RKA_RETURN_IF_ERR(current_device_info(&dev));
+    using T = BigTile<3, 4>;
+    int items = 0;
+    for (GemmArgs* g : {&a0, &a1}) {
+        if (!g->a_vec || !g->b_vec || !g->c_vec || g->kchunk <= 0 || g->k != g->ksplit * g->kchunk) return 0;
+        if (g->m % T::BM != 0 || g->n % T::BN != 0) return 0;
+        g->tiles_m = g->m / T::BM;
+        g->tiles = g->tiles_m * (g->n / T::BN);
+        items += g->tiles * g->ksplit;
+    }
+    if (dev->num_cus <= 0 || items % dev->num_cus != 0) return 0;
+    *launched = true;
+    auto kern = shift0 ? gemm_big_pair_kernel<3, 4, true> : gemm_big_pair_kernel<3, 4, false>;
+    RKA_RETURN_IF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, T::SMEM_BYTES));
+    hipLaunchKernelGGL(kern, dim3(items), dim3(T::NT), T::SMEM_BYTES, stream, a0, a1);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
 }  // namespace
 
 int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum,
@@ -751,6 +940,9 @@ int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hi
     if (p1.b.shift_T > 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: only the first product of a pair is remapped");
     const bool seg = a0.a.seg.len || a0.b.seg.len || a1.a.seg.len || a1.b.seg.len;
     if (seg) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: pair products take whole operands");
+    bool launched = false;
+    RKA_RETURN_IF_ERR(try_big_pair(a0, a1, p0.b.shift_T > 0, stream, &launched));
+    if (launched) return 0;
     const dim3 grid(a0.tiles * a0.ksplit + a1.tiles * a1.ksplit);
     if (p0.b.shift_T > 0)
         hipLaunchKernelGGL((gemm_f32_pair_kernel<true, false>), grid, dim3(NT), 0, stream, a0, a1);

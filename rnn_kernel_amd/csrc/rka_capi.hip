@@ -453,6 +453,11 @@ int rka_set_backward_chunks(int chunks) {
     return 0;
 }
 
+int rka_set_gemm_tiles(int mode) {
+    clear_error();
+    return set_gemm_tiles(mode);
+}
+
 int rka_set_spin_limit(int polls) {
     clear_error();
     if (polls < 0 || polls > kMaxSpinPolls)

@@ -63,6 +63,40 @@ def test_gemm_matches_float64(gpu, hip_lib, m, n, k, a_kmajor, b_kmajor):
     assert err <= 1e-6 * k + 1e-5, err
 
 
+@pytest.fixture
+def gemm_tiles(hip_lib):
+    """Restores the automatic GEMM tile choice after a test that forces one."""
+    from rnn_kernel_amd import _lib
+
+    yield _lib.set_gemm_tiles
+    _lib.set_gemm_tiles(0)
+
+
+def test_layer_backward_large_tiles_match_128_tiles(gpu, hip_lib, gemm_tiles):
+    """A c2-shaped layer (B=64, T=512, I=H=256) runs its weight-gradient pair
+    in 192x256 tiles; every output and gradient equals the 128x128 kernels'
+    bit for bit."""
+    from rnn_kernel_amd import GRU
+
+    print("layer large tiles vs 128 tiles B=64 T=512 I=H=256", flush=True)
+    torch.manual_seed(7)
+    model = GRU(256, 256).to(gpu)
+    x = torch.randn(64, 512, 256, device=gpu)
+    h0 = 0.1 * torch.randn(1, 64, 256, device=gpu)
+    results = []
+    for mode in (0, 1):
+        gemm_tiles(mode)
+        model.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        y, hn = model(xi, h0)
+        (y.sin().sum() + hn.sum()).backward()
+        torch.cuda.synchronize()
+        results.append([y.detach().clone(), hn.detach().clone(), xi.grad.clone()] +
+                       [p.grad.clone() for p in model.parameters()])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
 def test_gemm_unaligned_operands_use_scalar_path(gpu, hip_lib):
     """Operands offset by one float (not 16-byte aligned) and odd leading dims."""
     from rnn_kernel_amd import _lib
