@@ -708,55 +708,74 @@ __global__ __launch_bounds__(64 * WMW * WNW) void gemm_big_pair_kernel(GemmArgs 
 // member r takes slices r, r + kTeam, ... in order, then the team's sums are
 // added as a fixed tree, so the order is the same on every run.
 constexpr int kTeam = 8;
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int ksplit,
-                                                            int m, int n, int rot, float* __restrict__ c,
-                                                            int ldc, float* __restrict__ colsum, int vec) {
-    const size_t per_row = vec ? (size_t)(n / 4) : (size_t)n;
-    const size_t items = (size_t)m * per_row;
-    const size_t total = items + (colsum ? m : 0);
-    const int member = threadIdx.x % kTeam;
-    const size_t teams = (size_t)gridDim.x * (blockDim.x / kTeam);
-    for (size_t idx = (size_t)blockIdx.x * (blockDim.x / kTeam) + threadIdx.x / kTeam; idx < total; idx += teams) {
-        if (idx < items) {
-            const int o = (int)(idx / per_row);
-            const int src = rot ? (o + rot) % m : o;
-            if (vec) {
-                const int col = 4 * (int)(idx % per_row);
-                const float* pp = partial + (size_t)src * n + col;
-                float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-                for (int z = member; z < ksplit; z += kTeam) {
-                    const float4 v = *reinterpret_cast<const float4*>(pp + (size_t)z * m * n);
-                    s4.x += v.x;
-                    s4.y += v.y;
-                    s4.z += v.z;
-                    s4.w += v.w;
-                }
-#pragma unroll
-                for (int off = 1; off < kTeam; off <<= 1) {
-                    s4.x += __shfl_xor(s4.x, off, kTeam);
-                    s4.y += __shfl_xor(s4.y, off, kTeam);
-                    s4.z += __shfl_xor(s4.z, off, kTeam);
-                    s4.w += __shfl_xor(s4.w, off, kTeam);
-                }
-                if (member == 0) *reinterpret_cast<float4*>(c + (size_t)o * ldc + col) = s4;
-            } else {
-                const int col = (int)(idx % per_row);
-                float sum = 0.f;
-                for (int z = member; z < ksplit; z += kTeam) sum += partial[((size_t)z * m + src) * n + col];
-#pragma unroll
-                for (int off = 1; off < kTeam; off <<= 1) sum += __shfl_xor(sum, off, kTeam);
-                if (member == 0) c[(size_t)o * ldc + col] = sum;
+struct ReduceJob {
+    const float* partial;
+    int ksplit, m, n, rot;
+    float* c;
+    int ldc;
+    float* colsum;
+    int vec;
+    size_t items, total;  // row items (float4 or float), then m column sums
+};
+
+__device__ __forceinline__ void reduce_item(const ReduceJob& j, size_t idx, int member) {
+    const int m = j.m, n = j.n, ksplit = j.ksplit;
+    if (idx < j.items) {
+        const size_t per_row = j.vec ? (size_t)(n / 4) : (size_t)n;
+        const int o = (int)(idx / per_row);
+        const int src = j.rot ? (o + j.rot) % m : o;
+        if (j.vec) {
+            const int col = 4 * (int)(idx % per_row);
+            const float* pp = j.partial + (size_t)src * n + col;
+            float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int z = member; z < ksplit; z += kTeam) {
+                const float4 v = *reinterpret_cast<const float4*>(pp + (size_t)z * m * n);
+                s4.x += v.x;
+                s4.y += v.y;
+                s4.z += v.z;
+                s4.w += v.w;
             }
+#pragma unroll
+            for (int off = 1; off < kTeam; off <<= 1) {
+                s4.x += __shfl_xor(s4.x, off, kTeam);
+                s4.y += __shfl_xor(s4.y, off, kTeam);
+                s4.z += __shfl_xor(s4.z, off, kTeam);
+                s4.w += __shfl_xor(s4.w, off, kTeam);
+            }
+            if (member == 0) *reinterpret_cast<float4*>(j.c + (size_t)o * j.ldc + col) = s4;
         } else {
-            const int o = (int)(idx - items);
-            const int src = rot ? (o + rot) % m : o;
-            const float* cpart = partial + (size_t)ksplit * m * n;
+            const int col = (int)(idx % per_row);
             float sum = 0.f;
-            for (int z = member; z < ksplit; z += kTeam) sum += cpart[(size_t)z * m + src];
+            for (int z = member; z < ksplit; z += kTeam) sum += j.partial[((size_t)z * m + src) * n + col];
 #pragma unroll
             for (int off = 1; off < kTeam; off <<= 1) sum += __shfl_xor(sum, off, kTeam);
-            if (member == 0) colsum[o] = sum;
+            if (member == 0) j.c[(size_t)o * j.ldc + col] = sum;
         }
+    } else {
+        const int o = (int)(idx - j.items);
+        const int src = j.rot ? (o + j.rot) % m : o;
+        const float* cpart = j.partial + (size_t)ksplit * m * n;
+        float sum = 0.f;
+        for (int z = member; z < ksplit; z += kTeam) sum += cpart[(size_t)z * m + src];
+#pragma unroll
+        for (int off = 1; off < kTeam; off <<= 1) sum += __shfl_xor(sum, off, kTeam);
+        if (member == 0) j.colsum[o] = sum;
+    }
+}
+
+// The reductions of one or two split-K products in one launch: team items
+// [0, j0.total) belong to the first, the rest to the second (j1.total = 0
+// for one product).  A team's idx is uniform over its kTeam lanes, so the
+// shuffles stay within one job.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceJob j0, ReduceJob j1) {
+    const int member = threadIdx.x % kTeam;
+    const size_t teams = (size_t)gridDim.x * (blockDim.x / kTeam);
+    const size_t total = j0.total + j1.total;
+    for (size_t idx = (size_t)blockIdx.x * (blockDim.x / kTeam) + threadIdx.x / kTeam; idx < total; idx += teams) {
+        if (idx < j0.total)
+            reduce_item(j0, idx, member);
+        else
+            reduce_item(j1, idx - j0.total, member);
     }
 }
 
@@ -952,19 +971,48 @@ int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hi
     return 0;
 }
 
+namespace {
+ReduceJob reduce_job(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,
+                     float* colsum) {
+    ReduceJob j{};
+    j.partial = partial;
+    j.ksplit = ksplit_total;
+    j.m = m;
+    j.n = n;
+    j.rot = rot;
+    j.c = c;
+    j.ldc = ldc;
+    j.colsum = colsum;
+    j.vec = (n % 4 == 0 && ldc % 4 == 0 && aligned16(partial) && aligned16(c)) ? 1 : 0;
+    j.items = (size_t)m * (j.vec ? n / 4 : n);
+    j.total = j.items + (colsum ? m : 0);
+    return j;
+}
+
+int launch_reduce(const ReduceJob& j0, const ReduceJob& j1, hipStream_t stream) {
+    const size_t total = j0.total + j1.total;
+    const int blocks = (int)std::min<size_t>((total * kTeam + 255) / 256, 8192);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(std::max(blocks, 1)), dim3(256), 0, stream, j0, j1);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
+}
+
+ReduceJob reduce_job(const SplitProduct& p) {
+    return reduce_job(p.m, p.n, p.partial, p.ksplit, p.rot, p.c, p.ldc, p.colsum);
+}
+}  // namespace
+
 int splitk_reduce(const SplitProduct& p, hipStream_t stream) {
-    return splitk_reduce(p.m, p.n, p.partial, p.ksplit, p.rot, p.c, p.ldc, p.colsum, stream);
+    return launch_reduce(reduce_job(p), ReduceJob{}, stream);
+}
+
+int splitk_reduce_pair(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream) {
+    return launch_reduce(reduce_job(p0), reduce_job(p1), stream);
 }
 
 int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,
                   float* colsum, hipStream_t stream) {
-    const int vec = (n % 4 == 0 && ldc % 4 == 0 && aligned16(partial) && aligned16(c)) ? 1 : 0;
-    const size_t total = (size_t)m * (vec ? n / 4 : n) + (colsum ? m : 0);
-    const int blocks = (int)std::min<size_t>((total * kTeam + 255) / 256, 8192);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partial, ksplit_total, m, n,
-                       rot, c, ldc, colsum, vec);
-    RKA_RETURN_IF_HIP(hipGetLastError());
-    return 0;
+    return launch_reduce(reduce_job(m, n, partial, ksplit_total, rot, c, ldc, colsum), ReduceJob{}, stream);
 }
 
 }  // namespace rka

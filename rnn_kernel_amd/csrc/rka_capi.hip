@@ -367,8 +367,7 @@ int rka_gru_backward(const float* x, const float* h0, const float* w_ih, const f
             RKA_RETURN_IF_ERR(gemm_splitk_pair_partials(hh, ih, s));
         }
         StageScope scope(4, s);
-        RKA_RETURN_IF_ERR(splitk_reduce(hh, s));
-        RKA_RETURN_IF_ERR(splitk_reduce(ih, s));
+        RKA_RETURN_IF_ERR(splitk_reduce_pair(hh, ih, s));
     }
     if (dx) {
         // dX = G_i W_ih: A(m=bt, k=j) = g[bt, H+j]; B(n=i, k=j) = W_ih[j, i].

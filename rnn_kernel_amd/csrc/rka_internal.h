@@ -107,6 +107,9 @@ struct SplitProduct {
 // calls with the same slices.
 int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream);
 int splitk_reduce(const SplitProduct& p, hipStream_t stream);
+// Both products' reductions in one launch (the same results as two
+// splitk_reduce calls).
+int splitk_reduce_pair(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream);
 // rka_set_gemm_tiles (RKA_GEMM_TILES_AUTO or RKA_GEMM_TILES_128).
 int set_gemm_tiles(int mode);
 // Slices for a split-K product of about wgs_per_cu workgroups per CU
