@@ -156,16 +156,6 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
                                 int batch, int seq_len, int hidden_size,
                                 void* stream);
 
-/* Override the recurrence kernel choice for direction `dir` (0 forward,
- * 1 backward); affects later calls on all threads.  For tuning and tests.
- * kind 0: automatic (register-resident kernel when hidden_size <= 256, with
- *         the fewest batch rows per workgroup that make the grid resident,
- *         else the most, the grid then running in waves; LDS-tiled above);
- * kind 1: LDS-tiled; units = hidden units per workgroup (a divisor of 64,
- *         0 = auto), param = wavefronts holding (row, unit) pairs (1, 2, 4,
- *         0 = auto);
- * kind 2: register-resident; units = 64 (or 0), param = batch rows per
- *         workgroup (1, 2, 4, 0 = auto). */
 /* GEMM tile families (for tuning and A/B tests; affects later calls on all
  * threads).  RKA_GEMM_TILES_AUTO: the weight-gradient pair of
  * rka_gru_backward runs in 192x256 tiles, one twelve-wavefront workgroup
@@ -231,9 +221,26 @@ int rka_set_stall_block(int block);
  * in the reference (whose launches cannot abort). */
 int rka_recurrence_abort_count(unsigned long long* count);
 
+/* Override the recurrence kernel choice for direction `dir` (0 forward,
+ * 1 backward); affects later calls on all threads.  For tuning and tests.
+ * kind 0: automatic (register-resident kernel when hidden_size <= 256, with
+ *         the fewest batch rows per workgroup whose grid is resident, else
+ *         four rows and one resident launch per batch slice; LDS-tiled
+ *         above 256);
+ * kind 1: LDS-tiled; units = hidden units per workgroup (a divisor of 64,
+ *         0 = auto), param = wavefronts holding (row, unit) pairs (1, 2, 4,
+ *         0 = auto);
+ * kind 2: register-resident; units = 64 (or 0), param = batch rows per
+ *         workgroup (1, 2, 4, 0 = auto);
+ * kind 3: matrix-core forward (dir 0 only): 16 batch rows x 16 hidden units
+ *         per workgroup on v_mfma_f32_16x16x4_f32; batch a multiple of 16,
+ *         hidden_size a multiple of 32 up to 256 (units and param 0).  Never
+ *         chosen automatically: measured slower than the register kernel at
+ *         every batch tried (2.31 vs 2.11 us per step at B = 256, H = 256). */
 #define RKA_REC_AUTO 0
 #define RKA_REC_TILED 1
 #define RKA_REC_REGISTER 2
+#define RKA_REC_MFMA 3
 int rka_set_recurrence_config(int dir, int kind, int units, int param);
 
 /* Describe the decomposition the next recurrence call would use for this

@@ -116,7 +116,7 @@ def profile_read() -> dict:
     return {lib.rka_profile_stage_name(i).decode(): (ms[i], cnt[i]) for i in range(NUM_STAGES)}
 
 
-REC_KINDS = {0: "auto", 1: "tiled", 2: "register"}
+REC_KINDS = {0: "auto", 1: "tiled", 2: "register", 3: "mfma"}
 
 
 def describe_recurrence(direction: int, batch: int, hidden: int) -> dict:

@@ -436,8 +436,11 @@ int rka_set_recurrence_config(int dir, int kind, int units, int param) {
     } else if (kind == REC_REGISTER) {
         if (!ok_p || !(units == 0 || units == 64))
             return fail(RKA_ERR_INVALID_ARGUMENT, "register: units 64 (or 0), rows 1, 2 or 4 (0 = auto)");
+    } else if (kind == REC_MFMA) {
+        if (dir != 0 || units != 0 || param != 0)
+            return fail(RKA_ERR_INVALID_ARGUMENT, "mfma: forward only (dir 0), units and param 0");
     } else {
-        return fail(RKA_ERR_INVALID_ARGUMENT, "kind must be 0 (auto), 1 (tiled) or 2 (register)");
+        return fail(RKA_ERR_INVALID_ARGUMENT, "kind must be 0 (auto), 1 (tiled), 2 (register) or 3 (mfma)");
     }
     set_rec_override(dir, kind, units, param);
     return 0;

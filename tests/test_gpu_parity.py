@@ -185,24 +185,45 @@ def _layer_inputs(B, T, I, H, seed, h0_scale=1.0):
     return p, x, h0, dy, dhn
 
 
-@pytest.fixture(params=["auto", "tiled"])
+@pytest.fixture(params=["auto", "tiled", "mfma"])
 def rec_kind(request, hip_lib):
     """Run a test with the automatic recurrence choice (register-resident for
-    H <= 256) and again with the LDS-tiled kernels forced."""
+    H <= 256), again with the LDS-tiled kernels forced, and again with the
+    matrix-core forward forced (the backward automatic)."""
     from rnn_kernel_amd import _lib
 
     if request.param == "tiled":
         for d in (0, 1):
             _lib.set_recurrence_config(d, 1, 0, 0)
+    elif request.param == "mfma":
+        _lib.set_recurrence_config(0, 3, 0, 0)
     yield request.param
     for d in (0, 1):
         _lib.set_recurrence_config(d, 0, 0, 0)
 
 
-@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768)])
+def _mfma_applies(B, H):
+    """Shapes the matrix-core forward takes: whole 16-row groups, H a
+    multiple of 32 up to 256."""
+    return B % 16 == 0 and H % 32 == 0 and 32 <= H <= 256
+
+
+def _skip_unless_kind_applies(rec_kind, B, H):
+    if rec_kind == "mfma" and not _mfma_applies(B, H):
+        pytest.skip("the matrix-core forward takes batch % 16 == 0 and hidden_size in 32, 64, ..., 256")
+
+
+# shapes the matrix-core forward takes, one per K width (H / 32 = 1 .. 8),
+# with T = 1 and a c4-sized batch
+MFMA_SHAPES = [(16, 5, 8, 32), (32, 7, 16, 64), (48, 4, 8, 96), (16, 6, 4, 128), (64, 9, 16, 160),
+               (32, 3, 8, 192), (16, 4, 8, 224), (256, 6, 16, 256), (64, 1, 1, 256)]
+
+
+@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768)] + MFMA_SHAPES)
 def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
     from rnn_kernel_amd import GRUFunction, _lib
 
+    _skip_unless_kind_applies(rec_kind, B, H)
     print(f"layer vs oracle B={B} T={T} I={I} H={H} kind={rec_kind} "
           f"fwd={_lib.describe_recurrence(0, B, H)} bwd={_lib.describe_recurrence(1, B, H)}", flush=True)
     p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B * 1000 + T * 10 + H)
@@ -247,12 +268,14 @@ def backward_chunks(hip_lib):
     (2, 3, 2, 40, 8),      # more chunks asked than steps: clamped to T
     (8, 9, 4, 256, 3),     # H = 256 with groups on one XCD (plain publishing stores) across ranges
     (3, 8, 4, 200, 3),     # four slices, the last one partial, across ranges
+    (16, 9, 4, 256, 3),    # a whole 16-row group (the matrix-core forward when forced)
 ])
 def test_chunked_backward_matches_oracle(gpu, oracle, rec_kind, backward_chunks, B, T, I, H, chunks):
     """The backward in time chunks (recurrence per range, gradient GEMMs of a
     finished range on a second stream) against the oracle."""
     from rnn_kernel_amd import GRUFunction, _lib
 
+    _skip_unless_kind_applies(rec_kind, B, H)
     backward_chunks(chunks)
     print(f"chunked backward B={B} T={T} I={I} H={H} chunks={_lib.backward_chunks(T)} kind={rec_kind}", flush=True)
     assert _lib.backward_chunks(T) == min(chunks, T)
@@ -345,6 +368,7 @@ def test_timed_out_waits_abort_with_nan_in_every_unwritten_output(gpu, oracle, h
     import rnn_kernel_amd
     from rnn_kernel_amd import _lib
 
+    _skip_unless_kind_applies(rec_kind, B, H)
     I = 8
     p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B + T)
     f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
@@ -667,6 +691,24 @@ def test_recurrences_progress_beside_a_concurrent_kernel(gpu, B, H):
         for a, b in zip(solo, busy):
             assert torch.isfinite(b).all()
             assert torch.equal(a, b)
+
+
+def test_matrix_core_forward_is_forced_only(gpu, hip_lib):
+    """The automatic choice keeps the register-resident forward (four rows per
+    workgroup at B = 256); forcing kind 3 describes the matrix-core
+    decomposition: 16 groups of 16 rows x 16 slices of 16 units, one launch."""
+    from rnn_kernel_amd import _lib
+
+    assert _lib.describe_recurrence(0, 256, 256)["kind"] == "register"
+    _lib.set_recurrence_config(0, 3, 0, 0)
+    try:
+        d = _lib.describe_recurrence(0, 256, 256)
+        print("forced matrix-core forward at B=256 H=256:", d, flush=True)
+        assert d["kind"] == "mfma" and d["launches"] == 1 and (d["groups"], d["slices"]) == (16, 16)
+        with pytest.raises(_lib.RKAError):
+            _lib.describe_recurrence(0, 300, 256)  # not whole 16-row groups
+    finally:
+        _lib.set_recurrence_config(0, 0, 0, 0)
 
 
 @pytest.mark.parametrize("H,fwd_rows,bwd_rows", [(200, 2, 4), (256, 2, 2), (160, 4, 4), (64, 4, 2)])

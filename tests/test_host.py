@@ -57,9 +57,12 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     rc = hip_lib.rka_gru_forward(*([None] * 10), 0, 2, 8, 4, 4, None)
     assert rc == 1001 and "null tensor pointer" in _lib.last_error()
     assert hip_lib.rka_set_recurrence_config(2, 0, 0, 0) == 1001   # bad direction
-    assert hip_lib.rka_set_recurrence_config(0, 3, 0, 0) == 1001   # bad kind
+    assert hip_lib.rka_set_recurrence_config(0, 5, 0, 0) == 1001   # bad kind
     assert hip_lib.rka_set_recurrence_config(0, 1, 3, 0) == 1001   # units must divide 64
     assert hip_lib.rka_set_recurrence_config(1, 2, 0, 3) == 1001   # rows 1, 2 or 4
+    assert hip_lib.rka_set_recurrence_config(1, 3, 0, 0) == 1001   # the matrix-core kernel is forward only
+    assert hip_lib.rka_set_recurrence_config(0, 3, 16, 0) == 1001  # and takes no units / rows
+    assert hip_lib.rka_set_recurrence_config(0, 4, 0, 0) == 1001   # bad kind
     assert hip_lib.rka_set_recurrence_config(0, 0, 0, 0) == 0
     assert hip_lib.rka_set_backward_chunks(-1) == 1001
     assert hip_lib.rka_set_backward_chunks(9) == 1001
