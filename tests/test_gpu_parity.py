@@ -185,32 +185,29 @@ def _layer_inputs(B, T, I, H, seed, h0_scale=1.0):
     return p, x, h0, dy, dhn
 
 
-@pytest.fixture(params=["auto", "tiled", "mfma"])
+@pytest.fixture(params=["auto", "tiled"])
 def rec_kind(request, hip_lib):
     """Run a test with the automatic recurrence choice (register-resident for
-    H <= 256), again with the LDS-tiled kernels forced, and again with the
-    matrix-core forward forced (the backward automatic)."""
+    H <= 256) and again with the LDS-tiled kernels forced."""
     from rnn_kernel_amd import _lib
 
     if request.param == "tiled":
         for d in (0, 1):
             _lib.set_recurrence_config(d, 1, 0, 0)
-    elif request.param == "mfma":
-        _lib.set_recurrence_config(0, 3, 0, 0)
     yield request.param
     for d in (0, 1):
         _lib.set_recurrence_config(d, 0, 0, 0)
 
 
-def _mfma_applies(B, H):
-    """Shapes the matrix-core forward takes: whole 16-row groups, H a
-    multiple of 32 up to 256."""
-    return B % 16 == 0 and H % 32 == 0 and 32 <= H <= 256
+@pytest.fixture
+def mfma_forward(hip_lib):
+    """Forces the matrix-core forward (kind 3; the backward stays automatic)
+    for one test, then restores the automatic choice."""
+    from rnn_kernel_amd import _lib
 
-
-def _skip_unless_kind_applies(rec_kind, B, H):
-    if rec_kind == "mfma" and not _mfma_applies(B, H):
-        pytest.skip("the matrix-core forward takes batch % 16 == 0 and hidden_size in 32, 64, ..., 256")
+    _lib.set_recurrence_config(0, 3, 0, 0)
+    yield "mfma"
+    _lib.set_recurrence_config(0, 0, 0, 0)
 
 
 # shapes the matrix-core forward takes, one per K width (H / 32 = 1 .. 8),
@@ -221,9 +218,17 @@ MFMA_SHAPES = [(16, 5, 8, 32), (32, 7, 16, 64), (48, 4, 8, 96), (16, 6, 4, 128),
 
 @pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768)] + MFMA_SHAPES)
 def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
+    _check_layer_against_oracle(gpu, oracle, rec_kind, B, T, I, H)
+
+
+@pytest.mark.parametrize("B,T,I,H", MFMA_SHAPES)
+def test_layer_with_matrix_core_forward_matches_oracle(gpu, oracle, mfma_forward, B, T, I, H):
+    _check_layer_against_oracle(gpu, oracle, mfma_forward, B, T, I, H)
+
+
+def _check_layer_against_oracle(gpu, oracle, rec_kind, B, T, I, H):
     from rnn_kernel_amd import GRUFunction, _lib
 
-    _skip_unless_kind_applies(rec_kind, B, H)
     print(f"layer vs oracle B={B} T={T} I={I} H={H} kind={rec_kind} "
           f"fwd={_lib.describe_recurrence(0, B, H)} bwd={_lib.describe_recurrence(1, B, H)}", flush=True)
     p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B * 1000 + T * 10 + H)
@@ -268,14 +273,13 @@ def backward_chunks(hip_lib):
     (2, 3, 2, 40, 8),      # more chunks asked than steps: clamped to T
     (8, 9, 4, 256, 3),     # H = 256 with groups on one XCD (plain publishing stores) across ranges
     (3, 8, 4, 200, 3),     # four slices, the last one partial, across ranges
-    (16, 9, 4, 256, 3),    # a whole 16-row group (the matrix-core forward when forced)
+    (16, 9, 4, 256, 3),    # a whole 16-row group
 ])
 def test_chunked_backward_matches_oracle(gpu, oracle, rec_kind, backward_chunks, B, T, I, H, chunks):
     """The backward in time chunks (recurrence per range, gradient GEMMs of a
     finished range on a second stream) against the oracle."""
     from rnn_kernel_amd import GRUFunction, _lib
 
-    _skip_unless_kind_applies(rec_kind, B, H)
     backward_chunks(chunks)
     print(f"chunked backward B={B} T={T} I={I} H={H} chunks={_lib.backward_chunks(T)} kind={rec_kind}", flush=True)
     assert _lib.backward_chunks(T) == min(chunks, T)
@@ -365,10 +369,19 @@ def test_timed_out_waits_abort_with_nan_in_every_unwritten_output(gpu, oracle, h
     oracle, and the per-device count of aborted calls
     (rka_recurrence_abort_count) must grow by one per call, which
     check_recurrences() turns into RecurrenceAbortedError."""
+    _check_abort_path(gpu, oracle, hip_lib, rec_kind, B, T, H)
+
+
+@pytest.mark.parametrize("B,T,H", [(16, 32, 256), (64, 24, 256)])
+def test_timed_out_waits_abort_matrix_core_forward(gpu, oracle, hip_lib, mfma_forward, B, T, H):
+    """The forced-abort test with the matrix-core forward."""
+    _check_abort_path(gpu, oracle, hip_lib, mfma_forward, B, T, H)
+
+
+def _check_abort_path(gpu, oracle, hip_lib, rec_kind, B, T, H):
     import rnn_kernel_amd
     from rnn_kernel_amd import _lib
 
-    _skip_unless_kind_applies(rec_kind, B, H)
     I = 8
     p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B + T)
     f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
