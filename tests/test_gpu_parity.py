@@ -157,6 +157,7 @@ LAYER_SHAPES = [
     (300, 3, 8, 256),    # B x 4 workgroups not resident: four rows per workgroup, two batch-slice launches
     (130, 4, 6, 130),    # three slices, two rows per workgroup
     (400, 5, 4, 160),    # three slices at four rows not resident: batch-slice launches of 80 groups
+    (1, 3, 4, 768),      # the largest hidden size at one batch row (LDS-tiled, one unit per workgroup)
 ]
 
 
