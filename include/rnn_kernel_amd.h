@@ -211,6 +211,19 @@ int rka_set_spin_limit(int polls);
  * path deterministically. */
 int rka_set_stall_block(int block);
 
+/* How recurrence workgroups publish their exchange words.
+ * RKA_EXCHANGE_AUTO (the default): with plain stores, which stay in the
+ * XCD's L2, when a start-up check finds every workgroup of the exchange
+ * group on one XCD (the grid is laid out so that they are whenever it is
+ * still resident with the group count rounded up to a multiple of 8), else
+ * with agent-scope stores.  RKA_EXCHANGE_AGENT: always agent-scope stores
+ * (slower; the same results bit for bit).  Affects later launches on all
+ * threads.  No counterpart in the reference; exported so tests cover both
+ * store paths at every shape. */
+#define RKA_EXCHANGE_AUTO 0
+#define RKA_EXCHANGE_AGENT 1
+int rka_set_exchange_stores(int mode);
+
 /* Number of recurrence calls on the current device that aborted (a wait
  * gave up, see rka_set_spin_limit) since the library was loaded.  A call is
  * one direction of one layer (rka_gru_forward, rka_gru_backward or a

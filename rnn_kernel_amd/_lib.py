@@ -37,6 +37,7 @@ SIGNATURES = {
     "rka_set_backward_chunks": (_I, [_I]),
     "rka_set_spin_limit": (_I, [_I]),
     "rka_set_gemm_tiles": (_I, [_I]),
+    "rka_set_exchange_stores": (_I, [_I]),
     "rka_recurrence_abort_count": (_I, [ctypes.POINTER(ctypes.c_ulonglong)]),
     "rka_set_stall_block": (_I, [_I]),
     "rka_backward_chunks": (_I, [_I]),
@@ -149,6 +150,13 @@ def set_gemm_tiles(mode: int) -> None:
     """GEMM tile families: 0 = automatic (large persistent tiles where they
     divide evenly), 1 = 128x128 everywhere; see rka_set_gemm_tiles."""
     check(load().rka_set_gemm_tiles(mode), "rka_set_gemm_tiles")
+
+
+def set_exchange_stores(mode: int) -> None:
+    """Recurrence exchange stores: 0 = automatic (XCD-local plain stores
+    when a group shares one XCD), 1 = agent scope always; see
+    rka_set_exchange_stores."""
+    check(load().rka_set_exchange_stores(mode), "rka_set_exchange_stores")
 
 
 def set_stall_block(block: int) -> None:

@@ -96,7 +96,8 @@ __global__ __launch_bounds__(NTH) void gru_fwd_mfma_kernel(
     const int B = p.B, T = p.T, H = p.H;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
+    const rec::GroupCoords gc = rec::group_coords(p.S);
+    if (gc.g >= p.G) return;  // padding workgroup of a grid rounded up to whole XCDs
     const int g = gc.g, s = gc.s;
     const int col = lane & 15, kk = lane >> 4;
 
@@ -289,6 +290,7 @@ int mfma_choose(int dir, int batch, int hidden, const DeviceInfo& dev, RecConfig
     c.lds_bytes = 0;
     c.launches = (batch + per_launch - 1) / per_launch;
     c.batch_per_launch = per_launch;
+    c.resident = cap;
     *cfg = c;
     return 0;
 }
@@ -313,7 +315,8 @@ int mfma_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t str
     RKA_RETURN_IF_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kSpreadLds));
     void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                     (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
-    RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(NTH), args, kSpreadLds, stream));
+    const unsigned blocks = (unsigned)(grid_groups(c, c.groups) * c.slices);
+    RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(NTH), args, kSpreadLds, stream));
     return 0;
 }
 

@@ -117,7 +117,8 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
     const int B = p.B, T = p.T, H = p.H;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
+    const rec::GroupCoords gc = rec::group_coords(p.S);
+    if (gc.g >= p.G) return;  // padding workgroup of a grid rounded up to whole XCDs
     const int s = gc.s;
     const int row0 = gc.g * R;    // the group's first batch row
     const int u = s * 64 + lane;  // the owner lane's unit
@@ -568,7 +569,8 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     const int H3 = 3 * H;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-    const rec::GroupCoords gc = rec::group_coords(p.G, p.S);
+    const rec::GroupCoords gc = rec::group_coords(p.S);
+    if (gc.g >= p.G) return;  // padding workgroup of a grid rounded up to whole XCDs
     const int row0 = gc.g * R;  // the group's first batch row
     const int s = gc.s;
     const int u = s * 64 + lane;  // the owner lane's unit
@@ -971,6 +973,7 @@ int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_
     cfg->pair_waves = 0;
     cfg->chunk = chunk;
     cfg->lds_bytes = 0;
+    cfg->resident = chosen_cap;
     return 0;
 }
 
@@ -984,17 +987,16 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
                   a.xcc_words, a.xcc_tag, a.spin_limit, a.abort_count, a.stall_block};
     const void* k = kernel_ptr(dir, cap, c.rows, c.slices);
     if (k == nullptr) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: no kernel for this row count");
+    const unsigned blocks = (unsigned)(grid_groups(c, c.groups) * c.slices);
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                         (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
-        RKA_RETURN_IF_HIP(
-            hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(block_threads(dir, c.rows)), args, 0, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(block_threads(dir, c.rows)), args, 0, stream));
     } else {
         void* args[] = {(void*)&a.dy, (void*)&a.dhn, (void*)&a.reserve, (void*)&a.h0, (void*)&a.y,
                         (void*)&a.w_hh, (void*)&a.gout, (void*)&a.dh0, (void*)&a.exch, (void*)&a.abort_flag,
                         (void*)&prm};
-        RKA_RETURN_IF_HIP(
-            hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(block_threads(dir, c.rows)), args, 0, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(block_threads(dir, c.rows)), args, 0, stream));
     }
     return 0;
 }

@@ -105,7 +105,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
     const int wave = tid >> 6;
     const int pw = wave % PW;
     const int kc = wave / PW;
-    const GroupCoords gc = group_coords(p.G, p.S);
+    const GroupCoords gc = group_coords(p.S);
+    if (gc.g >= p.G) return;  // padding workgroup of a grid rounded up to whole XCDs
     const int g = gc.g;
     const int s = gc.s;
     const int pair = pw * 64 + lane;
@@ -252,7 +253,8 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_backward_kernel(
     const int wave = tid >> 6;
     const int pw = wave % PW;
     const int kc = wave / PW;
-    const GroupCoords gc = group_coords(p.G, p.S);
+    const GroupCoords gc = group_coords(p.S);
+    if (gc.g >= p.G) return;  // padding workgroup of a grid rounded up to whole XCDs
     const int g = gc.g;
     const int s = gc.s;
     const int pair = pw * 64 + lane;
@@ -477,6 +479,7 @@ int tiled_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixe
                 best_cfg.lds_bytes = lds;
                 best_cfg.launches = launches;
                 best_cfg.batch_per_launch = per_launch;
+                best_cfg.resident = cap;
             }
         }
     }
@@ -499,20 +502,19 @@ int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t st
     prm.abort_count = a.abort_count;
     prm.stall_block = a.stall_block;
     const void* k = kernel_ptr(dir, c.pair_waves);
+    const unsigned blocks = (unsigned)(grid_groups(c, c.groups) * c.slices);
     if (c.lds_bytes > 65536) {
         RKA_RETURN_IF_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, c.lds_bytes));
     }
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                         (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(rec::NTH), args,
-                                                     (unsigned)c.lds_bytes, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(rec::NTH), args, (unsigned)c.lds_bytes, stream));
     } else {
         void* args[] = {(void*)&a.dy, (void*)&a.dhn, (void*)&a.reserve, (void*)&a.h0, (void*)&a.y,
                         (void*)&a.w_hh, (void*)&a.gout, (void*)&a.dh0, (void*)&a.exch, (void*)&a.abort_flag,
                         (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(c.groups * c.slices), dim3(rec::NTH), args,
-                                                     (unsigned)c.lds_bytes, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(rec::NTH), args, (unsigned)c.lds_bytes, stream));
     }
     return 0;
 }

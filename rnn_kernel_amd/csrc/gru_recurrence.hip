@@ -29,6 +29,7 @@ struct Override {
 Override g_override[2];
 std::atomic<int> g_spin_limit{kDefaultSpinPolls};
 std::atomic<int> g_stall_block{-1};
+std::atomic<bool> g_agent_stores{false};  // no start-up XCD check: agent-scope stores
 
 std::mutex g_count_mutex;
 std::vector<unsigned long long*> g_count_ptr;  // per device: address of rka_rec_abort_count
@@ -50,6 +51,7 @@ int abort_counter(int dev, unsigned long long** out) {
 
 void set_rec_spin_limit(int polls) { g_spin_limit.store(polls > 0 ? polls : kDefaultSpinPolls); }
 void set_rec_stall_block(int block) { g_stall_block.store(block); }
+void set_rec_agent_stores(bool on) { g_agent_stores.store(on); }
 
 int rec_abort_count(unsigned long long* count) {
     const DeviceInfo* dev = nullptr;
@@ -67,6 +69,12 @@ int batch_per_resident_launch(int batch, int rows, int S, long cap) {
     long groups = cap / S;
     if (groups >= 8) groups -= groups % 8;
     return (int)std::min<long>(batch, groups * rows);
+}
+
+int grid_groups(const RecConfig& c, int groups) {
+    if (groups % 8 == 0) return groups;
+    const int padded = (groups + 7) / 8 * 8;
+    return (long)padded * c.slices <= c.resident ? padded : groups;
 }
 
 void set_rec_override(int dir, int kind, int units, int param) {
@@ -148,8 +156,8 @@ int launch_slices(int dir, const RecConfig& c, rec::Args a, unsigned long long* 
         s.y = off(a.y, (size_t)T * H);
         s.reserve = off(a.reserve, (size_t)T * 4 * H);
         s.exch = const_cast<unsigned long long*>(exch0) + 2 * (size_t)r0 * W;
-        const size_t blocks = (size_t)cs.groups * cs.slices;
-        s.xcc_words = blocks <= (size_t)rec::MAX_XCC_BLOCKS ? xcc_base : nullptr;
+        const size_t blocks = (size_t)grid_groups(cs, cs.groups) * cs.slices;
+        s.xcc_words = blocks <= (size_t)rec::MAX_XCC_BLOCKS && !g_agent_stores.load() ? xcc_base : nullptr;
         s.xcc_tag = (unsigned)((size_t)(T - a.t_end) * c.launches + k + 1);
         if (cs.kind == REC_REGISTER) {
             RKA_RETURN_IF_ERR(reg_launch(dir, cs, s, stream));
@@ -189,7 +197,7 @@ int launch_at(int dir, rec::Args& a, const RecState& st, bool zero_ws, hipStream
     // launch that continues the previous one keeps its slots (tags grow).
     if (zero_ws) {
         const size_t n_slots = (size_t)2 * a.B * (dir == 0 ? 1 : 3) * a.H;
-        const size_t blocks = (size_t)c.groups * c.slices;
+        const size_t blocks = (size_t)grid_groups(c, c.groups) * c.slices;
         const size_t n_xcc = blocks <= (size_t)rec::MAX_XCC_BLOCKS ? blocks : 0;
         const size_t n = n_slots + n_xcc;
         hipLaunchKernelGGL(fill_u64_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,

@@ -172,17 +172,21 @@ __device__ __forceinline__ unsigned xcc_id() {
 // in each XCD's dispatch order always makes progress (the earliest group
 // that is not fully resident has its missing members at the heads of their
 // XCDs' queues, behind groups that can finish).
-//   G a multiple of 8: the S members of group g are consecutive in the
+// The grid holds GX = gridDim.x / S groups, GX >= G:
+//   GX a multiple of 8: the S members of group g are consecutive in the
 //     dispatch order of one XCD: blocks x + 8 (l S + k), x = g mod 8,
-//     l = g / 8, k < S, so the group also shares that XCD's L2;
-//   otherwise: consecutive block ids g S .. g S + S - 1.
+//     l = g / 8, k < S, so the group also shares that XCD's L2.  A grid
+//     of G groups rounded up to whole multiples of 8 (GX > G) has padding
+//     workgroups, g >= G, which the kernels end before their first barrier;
+//   otherwise (GX = G): consecutive block ids g S .. g S + S - 1.
 struct GroupCoords {
     int g, s;           // group and slice of this workgroup
     int first, stride;  // the group's blocks: first + k stride, k < S
 };
-__device__ __forceinline__ GroupCoords group_coords(int G, int S) {
+__device__ __forceinline__ GroupCoords group_coords(int S) {
     const int b = blockIdx.x;
-    if (G % 8 == 0) {
+    const int GX = (int)gridDim.x / S;
+    if (GX % 8 == 0) {
         const int x = b % 8, q = b / 8, l = q / S, k = q % S;
         return {x + 8 * l, k, x + 8 * l * S, 8};
     }

@@ -455,6 +455,14 @@ int rka_set_backward_chunks(int chunks) {
     return 0;
 }
 
+int rka_set_exchange_stores(int mode) {
+    clear_error();
+    if (mode != RKA_EXCHANGE_AUTO && mode != RKA_EXCHANGE_AGENT)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "mode must be RKA_EXCHANGE_AUTO (0) or RKA_EXCHANGE_AGENT (1)");
+    set_rec_agent_stores(mode == RKA_EXCHANGE_AGENT);
+    return 0;
+}
+
 int rka_set_gemm_tiles(int mode) {
     clear_error();
     return set_gemm_tiles(mode);

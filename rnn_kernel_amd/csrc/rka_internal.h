@@ -135,7 +135,13 @@ struct RecConfig {
     int lds_bytes = 0;     // dynamic LDS (tiled) or 0
     int launches = 1;      // batch slices, one launch each
     int batch_per_launch = 0;
+    long resident = 0;     // workgroups of the chosen kernel resident on the device
 };
+// Exchange groups in the grid of a launch of `groups` groups: rounded up to
+// a multiple of 8 when that padded grid is still resident, so that each
+// group's workgroups share one XCD (rec::group_coords); the padding
+// workgroups exit at once.  Otherwise `groups`.
+int grid_groups(const RecConfig& c, int groups);
 // Batch rows per launch for a family whose grid of G groups of `rows` rows
 // and S slices holds at most `cap` resident workgroups (cap >= S): the whole
 // batch when it fits, else the most groups that fit, rounded down to a
@@ -150,6 +156,8 @@ constexpr int kDefaultSpinPolls = 1 << 24;
 constexpr int kMaxSpinPolls = 1 << 30;
 void set_rec_spin_limit(int polls);
 void set_rec_stall_block(int block);
+// rka_set_exchange_stores: true forces agent-scope exchange stores.
+void set_rec_agent_stores(bool on);
 // Number of recurrence launches on the current device that aborted since
 // the library was loaded (synchronises the device).
 int rec_abort_count(unsigned long long* count);

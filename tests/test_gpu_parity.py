@@ -227,6 +227,53 @@ def test_layer_with_matrix_core_forward_matches_oracle(gpu, oracle, mfma_forward
     _check_layer_against_oracle(gpu, oracle, mfma_forward, B, T, I, H)
 
 
+@pytest.fixture
+def agent_stores(hip_lib):
+    """Forces agent-scope exchange stores for one test, then restores the
+    automatic choice."""
+    from rnn_kernel_amd import _lib
+
+    _lib.set_exchange_stores(1)
+    yield "agent-scope stores"
+    _lib.set_exchange_stores(0)
+
+
+# register (H <= 256) and tiled (H = 512) recurrences; G = 1, 3, 4, 5 and 64 groups
+AGENT_SHAPES = [(1, 5, 8, 256), (3, 5, 7, 130), (4, 6, 8, 256), (5, 4, 8, 512), (64, 4, 16, 256)]
+
+
+@pytest.mark.parametrize("B,T,I,H", AGENT_SHAPES)
+def test_layer_with_agent_scope_exchange_matches_oracle(gpu, oracle, agent_stores, B, T, I, H):
+    """Every launch publishes with agent-scope stores (the path a group whose
+    workgroups span XCDs takes): the layer still matches the oracle."""
+    _check_layer_against_oracle(gpu, oracle, agent_stores, B, T, I, H)
+
+
+@pytest.mark.parametrize("B,T,I,H", AGENT_SHAPES)
+def test_exchange_store_paths_agree_bitwise(gpu, hip_lib, B, T, I, H):
+    """XCD-local plain stores and agent-scope stores move the same words: the
+    outputs and every gradient are equal bit for bit."""
+    from rnn_kernel_amd import GRUFunction, _lib
+
+    print(f"store paths B={B} T={T} I={I} H={H}", flush=True)
+    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B * 7 + H)
+    results = []
+    try:
+        for mode in (0, 1):
+            _lib.set_exchange_stores(mode)
+            xd = x.to(gpu).requires_grad_(True)
+            h0d = h0.to(gpu).requires_grad_(True)
+            pd = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
+            y, hn = GRUFunction.apply(xd, h0d, pd["weight_ih"], pd["weight_hh"], pd["bias_ih"], pd["bias_hh"])
+            torch.autograd.backward([y, hn], [dy.to(gpu), dhn.to(gpu)[None]])
+            torch.cuda.synchronize()
+            results.append([y.detach(), hn.detach(), xd.grad, h0d.grad] + [pd[k].grad for k in sorted(pd)])
+    finally:
+        _lib.set_exchange_stores(0)
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
 def _check_layer_against_oracle(gpu, oracle, rec_kind, B, T, I, H):
     from rnn_kernel_amd import GRUFunction, _lib
 
@@ -527,17 +574,18 @@ def test_batch_slices_of_resident_launches(gpu, hip_lib, B, H, launches):
             assert desc["groups"] % 8 == 0
 
 
-@pytest.mark.parametrize("B,H,local", [(64, 256, True), (8, 256, True), (4, 256, False), (3, 130, False)])
-def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H, local):
+@pytest.mark.parametrize("B,H", [(64, 256), (8, 256), (12, 256), (4, 256), (1, 256), (3, 130)])
+def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H):
     """Each recurrence workgroup records {XCC id, launch tag} in the workspace
     (after the two [B, 4H] exchange slots) and publishes with plain stores
     only when its exchange group shares one XCD.  Workgroups are dispatched
     to the 8 XCDs round-robin (consecutive block ids on consecutive XCDs,
-    from a starting XCD that varies by launch).  With a group count G that is
-    a multiple of 8 (the bench shape among them) the S members of group g
-    are blocks g % 8 + 8 ((g // 8) S + k), all on one XCD; otherwise they are
-    the consecutive blocks g S + k and take the agent-scope path.  Both give
-    the oracle's results in the layer tests."""
+    from a starting XCD that varies by launch).  The grid holds the G groups
+    rounded up to a multiple of 8 (at these sizes the padded grid is
+    resident): the S members of group g are blocks g % 8 + 8 ((g // 8) S + k),
+    all on one XCD, and the padding workgroups (g >= G) exit without
+    recording anything.  Small batches (G < 8) therefore exchange within one
+    XCD too; both store paths give the oracle's results in the layer tests."""
     from rnn_kernel_amd import _lib
 
     T = 3
@@ -558,22 +606,24 @@ def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H, local):
     assert torch.isfinite(hn).all()
     desc = _lib.describe_recurrence(0, B, H)
     groups, slices = desc["groups"], desc["slices"]
+    grid_groups = -(-groups // 8) * 8
     slots = (2 * B * 4 * H * 8 + 255) // 256 * 256
-    words = ws[slots:slots + 8 * groups * slices].cpu().view(torch.int64)
+    words = ws[slots:slots + 8 * grid_groups * slices].cpu().view(torch.int64)
     tags = (words >> 32).tolist()
     xcc = (words & 0xFFFFFFFF).tolist()
-    assert all(t == 1 for t in tags), tags
-    assert all(0 <= x < 16 for x in xcc)
-    def members(gi):
-        if groups % 8 == 0:
-            return [gi % 8 + 8 * ((gi // 8) * slices + k) for k in range(slices)]
-        return [gi * slices + k for k in range(slices)]
 
-    assert sorted(b for gi in range(groups) for b in members(gi)) == list(range(groups * slices))
+    def members(gi):
+        return [gi % 8 + 8 * ((gi // 8) * slices + k) for k in range(slices)]
+
+    real = sorted(b for gi in range(groups) for b in members(gi))
+    assert len(set(real)) == groups * slices and max(real) < grid_groups * slices
+    assert all(tags[b] == 1 for b in real), tags
+    assert all(tags[b] == 0 for b in set(range(grid_groups * slices)) - set(real)), tags
+    assert all(0 <= xcc[b] < 16 for b in real)
     on_one = [len({xcc[b] for b in members(gi)}) == 1 for gi in range(groups)]
-    print(f"B={B} H={H} groups={groups} slices={slices} xcc of the first blocks {xcc[:16]} "
-          f"groups on one XCD: {sum(on_one)}/{groups}", flush=True)
-    assert all(on_one) == local
+    print(f"B={B} H={H} groups={groups} grid groups={grid_groups} slices={slices} "
+          f"xcc of the first blocks {xcc[:16]} groups on one XCD: {sum(on_one)}/{groups}", flush=True)
+    assert all(on_one)
 
 
 # ----------------------------------- module vs torch.nn.GRU on the GPU ---

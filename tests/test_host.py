@@ -76,6 +76,9 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     assert hip_lib.rka_set_gemm_tiles(2) == 1001
     assert hip_lib.rka_set_gemm_tiles(-1) == 1001
     assert hip_lib.rka_set_gemm_tiles(1) == 0 and hip_lib.rka_set_gemm_tiles(0) == 0
+    assert hip_lib.rka_set_exchange_stores(2) == 1001
+    assert hip_lib.rka_set_exchange_stores(-1) == 1001
+    assert hip_lib.rka_set_exchange_stores(1) == 0 and hip_lib.rka_set_exchange_stores(0) == 0
 
 
 def test_backward_chunk_policy_without_gpu(hip_lib):
