@@ -351,7 +351,7 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
                     pv[r] = pvalid && rvalid[r];
                 }
                 bool ok = true;
-                rec::wait_words<R>(pp, pv, first_read, (unsigned)t, wc, ok);
+                rec::wait_words<R, R == 1>(pp, pv, first_read, (unsigned)t, wc, ok);
 #pragma unroll
                 for (int r = 0; r < R; ++r) hx[r] = pv[r] ? __uint_as_float((unsigned)first_read[r]) : 0.f;
                 if (!ok) s_abort = 1;
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
                 for (int t = t_stop; t < T; ++t) store_outputs(t);
             }
         }
-        hn[(size_t)orow * H + u] = aborted ? __builtin_nanf("") : h_prev;
+        hn[(unsigned)(orow * H + u)] = aborted ? __builtin_nanf("") : h_prev;  // B H < 2^31
     }
 }
 

@@ -249,7 +249,16 @@ __device__ __forceinline__ bool group_on_one_xcd(unsigned long long* words, int 
 // must point at a word that a valid lane of the same instruction loads: the
 // duplicate costs no request, whereas one stand-in address polled by every
 // wave of the grid would be a hot spot.
-template <int N>
+// UNIFORM: the wavefront polls as one (every lane reloads its words each
+// round until no lane is missing one; a tagged word does not change before
+// its reader has passed the step, so ready lanes reload the same value).
+// Otherwise each lane leaves the loop when its own words are in, which
+// costs some thirty scalar instructions of exec-mask bookkeeping per round.
+// Measured at c2 (same box, alternating pairs, µs per launch): forward (one
+// word per lane) 445.6-446.4 uniform vs 451.8-453.2 per lane; the backward
+// (several words per lane) 453.5 / 454.7 uniform vs 448.4 / 450.1, and the
+// four-row forward spills with it, so both keep the per-lane loop.
+template <int N, bool UNIFORM = false>
 __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[N], const bool (&valid)[N],
                                            unsigned long long (&w)[N], unsigned tag, const WaitCtl& wc, bool& ok) {
     auto ready = [&]() {
@@ -270,12 +279,15 @@ __device__ __forceinline__ void wait_words(const unsigned long long* const (&p)[
         for (int v = 0; v < N; ++v)
             if (valid[v] && (unsigned)(w[v] >> 32) != tag) w[v] = ((unsigned long long)tag << 32) | 0x7fc00000ull;
     };
-    if (!ok || ready()) return;
+    // wave-uniform: no lane is missing a word
+    auto all_ready = [&]() { return __builtin_amdgcn_ballot_w64(!ready()) == 0; };
+    if (!ok) return;
+    if (UNIFORM ? all_ready() : ready()) return;
     int spins = 0;
     for (;;) {
 #pragma unroll
         for (int v = 0; v < N; ++v) w[v] = load_word(p[v]);
-        if (ready()) break;
+        if (UNIFORM ? all_ready() : ready()) break;
         ++spins;
         if (spins >= wc.spin_limit) {
             raise_abort(wc);
