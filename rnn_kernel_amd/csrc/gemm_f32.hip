@@ -763,20 +763,45 @@ __device__ __forceinline__ void reduce_item(const ReduceJob& j, size_t idx, int 
     }
 }
 
-// The reductions of one or two split-K products in one launch: team items
-// [0, j0.total) belong to the first, the rest to the second (j1.total = 0
-// for one product).  A team's idx is uniform over its kTeam lanes, so the
-// shuffles stay within one job.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceJob j0, ReduceJob j1) {
+// The reductions of one or two split-K products by `blocks` workgroups of
+// 256 threads (this one is number `block`): team items [0, j0.total) belong
+// to the first, the rest to the second (j1.total = 0 for one product).  A
+// team's idx is uniform over its kTeam lanes, so the shuffles stay within
+// one job.
+__device__ __forceinline__ void reduce_range(const ReduceJob& j0, const ReduceJob& j1, int block, int blocks) {
+    constexpr int kTeamsPerBlock = 256 / kTeam;
     const int member = threadIdx.x % kTeam;
-    const size_t teams = (size_t)gridDim.x * (blockDim.x / kTeam);
+    const size_t teams = (size_t)blocks * kTeamsPerBlock;
     const size_t total = j0.total + j1.total;
-    for (size_t idx = (size_t)blockIdx.x * (blockDim.x / kTeam) + threadIdx.x / kTeam; idx < total; idx += teams) {
+    for (size_t idx = (size_t)block * kTeamsPerBlock + threadIdx.x / kTeam; idx < total; idx += teams) {
         if (idx < j0.total)
             reduce_item(j0, idx, member);
         else
             reduce_item(j1, idx - j0.total, member);
     }
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceJob j0, ReduceJob j1) {
+    reduce_range(j0, j1, blockIdx.x, gridDim.x);
+}
+
+// A direct product (workgroups [0, p.tiles), 128x128 tiles as in
+// gemm_f32_kernel) and the reductions of one or two split-K products (the
+// remaining workgroups) in one launch.  The backward's input gradient and
+// its weight-gradient reductions are independent: the reductions stream
+// partial sums from HBM while the product keeps the matrix cores busy, on
+// the workgroup slots the product's tiles leave free.
+template <int AK, int BKM>
+__global__ __launch_bounds__(NT) void gemm_direct_reduce_kernel(GemmArgs p, ReduceJob j0, ReduceJob j1) {
+    static_assert(NT == 256, "reduction teams assume 256-thread workgroups");
+    __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<AK, kDirectBK>()];
+    if ((int)blockIdx.x >= p.tiles) {
+        reduce_range(j0, j1, (int)blockIdx.x - p.tiles, (int)gridDim.x - p.tiles);
+        return;
+    }
+    int bx, by;
+    direct_coords(p, blockIdx.x, bx, by);
+    gemm_tile<AK, BKM, false, false, false, kDirectBK>(p, bx, by, 0, smem);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1008,6 +1033,45 @@ int splitk_reduce(const SplitProduct& p, hipStream_t stream) {
 
 int splitk_reduce_pair(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream) {
     return launch_reduce(reduce_job(p0), reduce_job(p1), stream);
+}
+
+int gemm_direct_reduce_pair(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, float* c, int ldc,
+                            const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream) {
+    if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
+    if (!a.ptr || !b.ptr || !c) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: null operand");
+    if (a.seg.len || b.seg.len || b.shift_T > 0) {
+        RKA_RETURN_IF_ERR(splitk_reduce_pair(p0, p1, stream));
+        return gemm_direct(m, n, k, a, b, nullptr, c, ldc, stream);
+    }
+    const DeviceInfo* dev = nullptr;
+    RKA_RETURN_IF_ERR(current_device_info(&dev));
+    GemmArgs args{};
+    args.a = a;
+    args.b = b;
+    args.m = m;
+    args.n = n;
+    args.k = k;
+    args.kchunk = (k + kDirectBK - 1) / kDirectBK * kDirectBK;
+    args.c = c;
+    args.ldc = ldc;
+    args.c_vec = (ldc % 4 == 0 && aligned16(c)) ? 1 : 0;
+    finish_args<false>(args, 1, vec_ok(a, m, k), vec_ok(b, n, k));
+    // one reducing workgroup per CU: with the product's tiles at up to two
+    // per CU they run beside them, in the third workgroup slot
+    const long reducers = dev->num_cus > 0 ? dev->num_cus : 256;
+    if ((long long)args.tiles + reducers > 0x7fffffff) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
+    const dim3 grid((unsigned)(args.tiles + reducers));
+    const ReduceJob j0 = reduce_job(p0), j1 = reduce_job(p1);
+    if (!a.kmajor && !b.kmajor)
+        hipLaunchKernelGGL((gemm_direct_reduce_kernel<0, 0>), grid, dim3(NT), 0, stream, args, j0, j1);
+    else if (!a.kmajor)
+        hipLaunchKernelGGL((gemm_direct_reduce_kernel<0, 1>), grid, dim3(NT), 0, stream, args, j0, j1);
+    else if (!b.kmajor)
+        hipLaunchKernelGGL((gemm_direct_reduce_kernel<1, 0>), grid, dim3(NT), 0, stream, args, j0, j1);
+    else
+        hipLaunchKernelGGL((gemm_direct_reduce_kernel<1, 1>), grid, dim3(NT), 0, stream, args, j0, j1);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    return 0;
 }
 
 int splitk_reduce(int m, int n, const float* partial, int ksplit_total, int rot, float* c, int ldc,

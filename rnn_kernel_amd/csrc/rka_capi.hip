@@ -366,15 +366,17 @@ int rka_gru_backward(const float* x, const float* h0, const float* w_ih, const f
             StageScope scope(3, s);
             RKA_RETURN_IF_ERR(gemm_splitk_pair_partials(hh, ih, s));
         }
-        StageScope scope(4, s);
-        RKA_RETURN_IF_ERR(splitk_reduce_pair(hh, ih, s));
-    }
-    if (dx) {
+        if (!dx) {
+            StageScope scope(4, s);
+            return splitk_reduce_pair(hh, ih, s);
+        }
         // dX = G_i W_ih: A(m=bt, k=j) = g[bt, H+j]; B(n=i, k=j) = W_ih[j, i].
+        // One launch with the reductions, which run beside its tiles (stage
+        // dx_gemm; dw_reduce stays empty).
         GemmOperand ga{g + H, 4 * H, 0, 0, nullptr};
         GemmOperand wk{w_ih, I, 1, 0, nullptr};
         StageScope scope(5, s);
-        RKA_RETURN_IF_ERR(gemm_direct(K, I, 3 * H, ga, wk, nullptr, dx, I, s));
+        return gemm_direct_reduce_pair(K, I, 3 * H, ga, wk, dx, I, hh, ih, s);
     }
     return 0;
 }

@@ -110,6 +110,10 @@ int splitk_reduce(const SplitProduct& p, hipStream_t stream);
 // Both products' reductions in one launch (the same results as two
 // splitk_reduce calls).
 int splitk_reduce_pair(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream);
+// gemm_direct (no bias) and splitk_reduce_pair(p0, p1) in one launch: the
+// same results as the two calls.
+int gemm_direct_reduce_pair(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, float* c, int ldc,
+                            const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream);
 // rka_set_gemm_tiles (RKA_GEMM_TILES_AUTO or RKA_GEMM_TILES_128).
 int set_gemm_tiles(int mode);
 // Slices for a split-K product of about wgs_per_cu workgroups per CU

@@ -97,6 +97,29 @@ def test_layer_backward_large_tiles_match_128_tiles(gpu, hip_lib, gemm_tiles):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("B,T,I,H", [(64, 512, 256, 256), (5, 7, 3, 33), (16, 9, 8, 130)])
+def test_weight_gradients_with_and_without_dx_agree_bitwise(gpu, hip_lib, B, T, I, H):
+    """With dx the weight-gradient reductions run in the input-gradient GEMM's
+    launch; without it (x needs no gradient) in a launch of their own.  The
+    weight and bias gradients are equal bit for bit."""
+    from rnn_kernel_amd import GRUFunction
+
+    print(f"dW with / without dx B={B} T={T} I={I} H={H}", flush=True)
+    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=B + T + I + H)
+    results = []
+    for need_dx in (True, False):
+        xd = x.to(gpu).requires_grad_(need_dx)
+        h0d = h0.to(gpu).requires_grad_(True)
+        pd = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
+        y, hn = GRUFunction.apply(xd, h0d, pd["weight_ih"], pd["weight_hh"], pd["bias_ih"], pd["bias_hh"])
+        torch.autograd.backward([y, hn], [dy.to(gpu), dhn.to(gpu)[None]])
+        torch.cuda.synchronize()
+        assert (xd.grad is not None) == need_dx
+        results.append([h0d.grad] + [pd[k].grad for k in sorted(pd)])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
 def test_gemm_unaligned_operands_use_scalar_path(gpu, hip_lib):
     """Operands offset by one float (not 16-byte aligned) and odd leading dims."""
     from rnn_kernel_amd import _lib
