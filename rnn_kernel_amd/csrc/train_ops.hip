@@ -16,6 +16,19 @@ constexpr int kThreads = 256;
 constexpr int kMaxReduceBlocks = 2048;   // partial sums of a loss reduction
 constexpr int kHeadBlocks = 512;         // row ranges of the head's dw reduction
 
+// Sum over the block's threads in a fixed order: each wavefront's 64 values
+// by a butterfly of lane exchanges, then the four wavefront sums in order
+// (one barrier instead of a tree of eight); valid in every thread.
+// `scratch` holds kThreads / 64 floats.
+__device__ __forceinline__ float block_sum_waves(float v, float* scratch) {
+    static_assert(kThreads == 256, "four wavefronts");
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+}
+
 // Sum over the block's threads in a fixed tree order; the result is valid in
 // thread 0.  `scratch` holds kThreads floats.
 __device__ __forceinline__ float block_sum(float v, float* scratch) {
@@ -47,7 +60,7 @@ __device__ __forceinline__ float4 load_streaming(const float4* p) {
 __global__ __launch_bounds__(kThreads) void mse_partial_kernel(const float* __restrict__ pred,
                                                                const float* __restrict__ target, size_t n,
                                                                size_t chunk, int vec, float* __restrict__ partial) {
-    __shared__ float scratch[kThreads];
+    __shared__ float scratch[kThreads / 64];
     const size_t beg = (size_t)blockIdx.x * chunk;
     const size_t end = beg + chunk < n ? beg + chunk : n;
     float acc = 0.f;
@@ -77,17 +90,26 @@ __global__ __launch_bounds__(kThreads) void mse_partial_kernel(const float* __re
             acc = fmaf(d, d, acc);
         }
     }
-    const float s = block_sum(acc, scratch);
+    const float s = block_sum_waves(acc, scratch);
     if (threadIdx.x == 0) partial[blockIdx.x] = s;
 }
 
-// loss[0] = (sum of the nb partials, thread t summing t, t + 256, ... in
-// order, then the fixed tree) / n
+// loss[0] = (sum of the nb <= kMaxReduceBlocks partials, thread t summing
+// t, t + 256, ... in order, then the fixed tree) / n.  The thread's loads are
+// all issued before the additions (one memory latency instead of eight).
 __global__ __launch_bounds__(kThreads) void mse_finish_kernel(const float* __restrict__ partial, int nb, size_t n,
                                                               float* __restrict__ loss) {
     __shared__ float scratch[kThreads];
+    constexpr int kPer = kMaxReduceBlocks / kThreads;
+    float v[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int i = (int)threadIdx.x + r * kThreads;
+        v[r] = i < nb ? partial[i] : 0.f;
+    }
     float acc = 0.f;
-    for (int i = threadIdx.x; i < nb; i += kThreads) acc += partial[i];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) acc += v[r];
     const float s = block_sum(acc, scratch);
     if (threadIdx.x == 0) loss[0] = s / (float)n;
 }
