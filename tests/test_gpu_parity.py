@@ -240,7 +240,8 @@ MFMA_SHAPES = [(16, 5, 8, 32), (32, 7, 16, 64), (48, 4, 8, 96), (16, 6, 4, 128),
                (32, 3, 8, 192), (16, 4, 8, 224), (256, 6, 16, 256), (64, 1, 1, 256)]
 
 
-@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768)] + MFMA_SHAPES)
+@pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768), (200, 2, 8, 768),
+                                     (256, 2, 8, 512)] + MFMA_SHAPES)
 def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
     _check_layer_against_oracle(gpu, oracle, rec_kind, B, T, I, H)
 
