@@ -385,6 +385,30 @@ __device__ __forceinline__ const float* dma_src(const GemmOperand& op, int r0, i
     }
 }
 
+// s_waitcnt vmcnt(n) with expcnt / lgkmcnt left at their maxima (gfx9
+// encoding: vmcnt bits 3:0); n is wave-uniform.  n above 15 waits for
+// everything (never less than asked).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+        case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+        case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+        case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+        case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+        case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+        case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+        case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+        case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+        case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+        case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+        case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+        case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+        case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
 template <int AK, int BKM, bool BSHIFT, bool SEG>
 __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, int kbeg, int nkb, int tid, int lane,
                                              int wm, int wn, bool colsum, float& cs, float* smem,
@@ -401,20 +425,16 @@ __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, 
             lds_dma16(dma_src<BKM, BSHIFT, SEG, true>(p.b, n0, k0, s0 + lane), b_stage(st) + 4 * s0);
         }
     };
-    issue(0, 0);
-    if (nkb > 1) issue(1, 1);
+    for (int kb = 0; kb < kDmaStages - 1 && kb < nkb; ++kb) issue(kb, kb);
     for (int kb = 0; kb < nkb; ++kb) {
-        // this wave's four loads of stage kb are done once at most the next
-        // stage's four are outstanding (gfx9 s_waitcnt: vmcnt in bits 3:0,
-        // expcnt and lgkmcnt left at their maxima)
-        if (kb + 1 < nkb)
-            __builtin_amdgcn_s_waitcnt(0x0F74);
-        else
-            __builtin_amdgcn_s_waitcnt(0x0F70);
+        // this wave's four loads of stage kb are done once at most those of
+        // the later stages already issued (up to kDmaStages - 2) are
+        // outstanding
+        wait_vmcnt(4 * min(kDmaStages - 2, nkb - 1 - kb));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kb + 2 < nkb) issue(kb + 2, (kb + 2) % kDmaStages);
+        if (kb + kDmaStages - 1 < nkb) issue(kb + kDmaStages - 1, (kb + kDmaStages - 1) % kDmaStages);
         mma_tile<AK == 1 ? 1 : 2, 16, BM, BKM == 1 ? 1 : 2>(a_stage(kb % kDmaStages), b_stage(kb % kDmaStages), lane,
                                                            wm, wn, tid, colsum, cs, acc);
     }
@@ -587,29 +607,6 @@ struct BigTile {
     static_assert(D >= 3, "the ring needs three stages");
 };
 
-// s_waitcnt vmcnt(n) with expcnt / lgkmcnt left at their maxima (gfx9
-// encoding: vmcnt bits 3:0); n is wave-uniform.  n above 15 waits for
-// everything (never less than asked).
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    switch (n) {
-        case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-        case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-        case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-        case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-        case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-        case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
-        case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-        case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-        case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
-        case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
-        case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-        case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
-        case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
-        case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
-        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    }
-}
 
 // One item (split_coords(p, id)) of a split-K product of k-major operands.
 template <int WMW, int WNW, bool BSHIFT>
