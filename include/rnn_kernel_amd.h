@@ -279,6 +279,9 @@ int rka_eval_gate_functions(const float* x, float* sigmoid_out, float* tanh_out,
  * Stage ids: 0 input GEMM, 1 forward recurrence, 2 backward recurrence,
  * 3 dW_hh and dW_ih split-K products (one launch unless the backward runs
  * in time chunks), 4 their split-K reductions into dW and db, 5 dx GEMM.
+ * When dx is requested from an unchunked backward, the reductions run in
+ * the dx GEMM's launch and are reported under stage 5 (stage 4 then has no
+ * launches).
  */
 #define RKA_NUM_STAGES 6
 int rka_profile_enable(int on);
