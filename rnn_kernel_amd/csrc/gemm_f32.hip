@@ -237,9 +237,14 @@ __device__ __forceinline__ void direct_coords(const GemmArgs& p, int id, int& bx
 // swizzled row form of the direct-to-LDS loads (swz_slot below, BK = 16).
 // A in form 2 has the block rows of the row form; B in form 2 the block
 // columns of the k form.
-template <int ALF, int BK, int KS = LDSP, int BLF = 1>
+struct NoStep {
+    __device__ void operator()() const {}
+};
+// `mid` runs after the tile's first MFMA step (the DMA ring issues the loads
+// into the stage it frees there, once the matrix cores are busy).
+template <int ALF, int BK, int KS = LDSP, int BLF = 1, typename F = NoStep>
 __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int lane, int wm, int wn, int tid,
-                                         bool colsum, float& cs, floatx4 (&acc)[4][4]) {
+                                         bool colsum, float& cs, floatx4 (&acc)[4][4], F mid = F{}) {
     static_assert((ALF != 2 && BLF != 2) || BK == 16, "swizzled row form holds 16-deep tiles");
     if constexpr (ALF == 1) {
         if (colsum && tid < BM) {
@@ -286,6 +291,11 @@ __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int l
                     const float bv = BLF == 2 ? fb[q][b][j] : fb[q][j][b];
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[a][b], 0, 0, 0);
                 }
+            }
+            if (q == 0 && j == 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                mid();
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -434,9 +444,20 @@ __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, 
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kb + kDmaStages - 1 < nkb) issue(kb + kDmaStages - 1, (kb + kDmaStages - 1) % kDmaStages);
+        // the stage consumed at kb - 1 is free: every wave is past its reads
+        // of it (the barrier).  Row-major A (the direct products): refilled
+        // after this stage's first MFMA step (dx at c2: 110-112 vs 113-114
+        // us); k-major A (the split-K column sums) before the MFMAs, which
+        // keeps those kernels at three workgroups per CU.
+        auto refill = [&]() {
+            if (kb + kDmaStages - 1 < nkb) issue(kb + kDmaStages - 1, (kb + kDmaStages - 1) % kDmaStages);
+        };
+        if constexpr (AK == 1) refill();
         mma_tile<AK == 1 ? 1 : 2, 16, BM, BKM == 1 ? 1 : 2>(a_stage(kb % kDmaStages), b_stage(kb % kDmaStages), lane,
-                                                           wm, wn, tid, colsum, cs, acc);
+                                                           wm, wn, tid, colsum, cs, acc,
+                                                           [&]() {
+                                                               if constexpr (AK == 0) refill();
+                                                           });
     }
 }
 
