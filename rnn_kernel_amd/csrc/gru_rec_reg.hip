@@ -548,20 +548,31 @@ __device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
 // The owner keeps its per-step G stores: the ninth-wavefront form of the
 // forward, with the own entries' weights in LDS to fit 168 VGPRs, measured
 // 0.50-0.51 vs 0.48 ms per c2 launch.
-template <int S, int R>
-__global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
+//
+// NWB wavefronts (8, or 16 for one row: 64 j-groups of 3 own and 3 (S - 1)
+// remote entries, one poll register per lane, 122 VGPRs at S = 4).  The
+// remote FMAs are bound by the SIMD's VALU issue rate (running them twice
+// per step added 144 FMA instructions per SIMD and ~139 ns), so sixteen
+// wavefronts issue the same instructions per SIMD; measured at c2 (same
+// box, three pairs) the one-row backward took 444.2-447.0 vs 447.5-448.4
+// us per launch and the step 1.355-1.358 vs 1.361-1.364 ms.
+template <int S, int R, int NWB = NW>
+__global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
     const float* __restrict__ h0, const float* __restrict__ y, const float* __restrict__ w_hh,
     float* __restrict__ gout, float* __restrict__ dh0, unsigned long long* __restrict__ exch,
     int* __restrict__ abort_flag, RegParams p) {
     static_assert(R == 1 || R == 2 || R == 4, "rows per workgroup");
-    constexpr int RE = 6 * (S - 1);                  // remote entries per j-group
+    static_assert(NWB == 8 || NWB == 16, "wavefronts per workgroup");
+    constexpr int NJ = 4 * NWB;                      // j-groups (sixteen-lane rows)
+    constexpr int OWN = 192 / NJ;                    // own entries per j-group (6 or 3)
+    constexpr int RE = OWN * (S - 1);                // remote entries per j-group
     constexpr int WE = 4 * RE;                       // remote entries polled per wave and row
     constexpr int GR = RE > 0 ? (RE + 3) / 4 * 4 : 4;  // LDS row of a j-group's polled words
     constexpr int NW2 = WE > 64 ? 2 : 1;             // poll registers per row
-    __shared__ __attribute__((aligned(16))) float part[2][NW][R][64];
-    __shared__ __attribute__((aligned(16))) float gloc[R][32][8];      // own G words by j-group (6 used)
-    __shared__ __attribute__((aligned(16))) float grem[NW][R][4][GR];  // per wave and row: polled words by j-group
+    __shared__ __attribute__((aligned(16))) float part[2][NWB][R][64];
+    __shared__ __attribute__((aligned(16))) float gloc[R][NJ][OWN > 4 ? 8 : 4];  // own G words by j-group
+    __shared__ __attribute__((aligned(16))) float grem[NWB][R][4][GR];  // per wave and row: polled words by j-group
     __shared__ int s_abort;
     __shared__ int s_local;
 
@@ -593,7 +604,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
     };
 
     // W_hh[j][ub .. ub + 3] for the j-group's own (wl) and remote (wm) entries
-    float wl[6][4], wm[RE > 0 ? RE : 1][4];
+    float wl[OWN][4], wm[RE > 0 ? RE : 1][4];
     const bool vec = p.wvec != 0;
     auto load4 = [&](int jr, bool ok, float (&d)[4]) {
         const float* src = w_hh + (size_t)jr * H + ub;
@@ -609,9 +620,9 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         }
     };
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
+    for (int i = 0; i < OWN; ++i) {
         bool ok;
-        const int jr = own_row(6 * J + i, ok);
+        const int jr = own_row(OWN * J + i, ok);
         load4(jr, ok, wl[i]);
     }
 #pragma unroll
@@ -712,7 +723,7 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
                 const int e = 64 * c + lane;
-                gloc[wave][e / 6][e % 6] = gv[c];
+                gloc[wave][e / OWN][e % OWN] = gv[c];
             }
         }
     };
@@ -730,9 +741,14 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[r][0][v] = acc[r][1][v] = 0.f;
             const float4 a = *reinterpret_cast<const float4*>(&gloc[r][J][0]);
-            const float4 b = *reinterpret_cast<const float4*>(&gloc[r][J][4]);
-            const float g[6] = {a.x, a.y, a.z, a.w, b.x, b.y};
-            fma_group(r, g, 6, wl);
+            if constexpr (OWN == 6) {
+                const float4 b = *reinterpret_cast<const float4*>(&gloc[r][J][4]);
+                const float g[6] = {a.x, a.y, a.z, a.w, b.x, b.y};
+                fma_group(r, g, 6, wl);
+            } else {
+                const float g[3] = {a.x, a.y, a.z};
+                fma_group(r, g, 3, wl);
+            }
         }
     };
     // the first poll reads of step i, issued ahead of its own-entry FMAs
@@ -831,7 +847,13 @@ __global__ __launch_bounds__(NTH) void gru_bwd_local_kernel(
         __syncthreads();
         // @probe:synced
         const bool abort_now = s_abort != 0;  // read with the partials
-        if (owner) dh = ddirect + rec::tree8([&](int w2) { return part[i & 1][w2][wave][lane]; });
+        if (owner) {
+            const float lo = rec::tree8([&](int w2) { return part[i & 1][w2][wave][lane]; });
+            if constexpr (NWB == 16)
+                dh = ddirect + (lo + rec::tree8([&](int w2) { return part[i & 1][8 + w2][wave][lane]; }));
+            else
+                dh = ddirect + lo;
+        }
         const bool more = i + 1 < i1;
         if (more) pointwise(i + 1, nxt);
         // @probe:published
@@ -883,7 +905,7 @@ template <int S>
 const void* local_ptr(int dir, int rows, bool io) {
     if (dir == 1) {
         switch (rows) {
-            case 1: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 1>);
+            case 1: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 1, 16>);
             case 2: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 2>);
             default: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 4>);
         }
@@ -901,7 +923,10 @@ const void* local_ptr(int dir, int rows, bool io) {
 // with one row per workgroup.
 bool uses_io(int dir, int rows) { return dir == 0 && rows == 1; }
 
-int block_threads(int dir, int rows) { return uses_io(dir, rows) ? NTH + 64 : NTH; }
+int block_threads(int dir, int rows) {
+    if (dir == 1 && rows == 1) return 16 * 64;  // the one-row backward: sixteen wavefronts
+    return uses_io(dir, rows) ? NTH + 64 : NTH;
+}
 
 // The local-slice kernels: S slices, 1, 2 or 4 batch rows per workgroup.
 const void* kernel_ptr(int dir, int cap, int rows, int slices) {
