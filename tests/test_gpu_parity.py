@@ -241,7 +241,7 @@ MFMA_SHAPES = [(16, 5, 8, 32), (32, 7, 16, 64), (48, 4, 8, 96), (16, 6, 4, 128),
 
 
 @pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768), (200, 2, 8, 768),
-                                     (256, 2, 8, 512)] + MFMA_SHAPES)
+                                     (256, 2, 8, 512), (83, 4, 8, 130)] + MFMA_SHAPES)
 def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
     _check_layer_against_oracle(gpu, oracle, rec_kind, B, T, I, H)
 
@@ -598,8 +598,9 @@ def test_batch_slices_of_resident_launches(gpu, hip_lib, B, H, launches):
             assert desc["groups"] % 8 == 0
 
 
-@pytest.mark.parametrize("B,H", [(64, 256), (8, 256), (12, 256), (4, 256), (1, 256), (3, 130)])
-def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H):
+@pytest.mark.parametrize("B,H,padded", [(64, 256, True), (8, 256, True), (12, 256, True), (4, 256, True),
+                                        (1, 256, True), (3, 130, True), (83, 130, False)])
+def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H, padded):
     """Each recurrence workgroup records {XCC id, launch tag} in the workspace
     (after the two [B, 4H] exchange slots) and publishes with plain stores
     only when its exchange group shares one XCD.  Workgroups are dispatched
@@ -609,7 +610,10 @@ def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H):
     resident): the S members of group g are blocks g % 8 + 8 ((g // 8) S + k),
     all on one XCD, and the padding workgroups (g >= G) exit without
     recording anything.  Small batches (G < 8) therefore exchange within one
-    XCD too; both store paths give the oracle's results in the layer tests."""
+    XCD too.  A grid resident only unpadded (83 groups of 3 workgroups on
+    256 CUs, not 88) keeps consecutive blocks g S + k, spread over XCDs, and
+    those groups publish with agent-scope stores.  Both store paths give the
+    oracle's results in the layer tests."""
     from rnn_kernel_amd import _lib
 
     T = 3
@@ -630,14 +634,16 @@ def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H):
     assert torch.isfinite(hn).all()
     desc = _lib.describe_recurrence(0, B, H)
     groups, slices = desc["groups"], desc["slices"]
-    grid_groups = -(-groups // 8) * 8
+    grid_groups = -(-groups // 8) * 8 if padded else groups
     slots = (2 * B * 4 * H * 8 + 255) // 256 * 256
     words = ws[slots:slots + 8 * grid_groups * slices].cpu().view(torch.int64)
     tags = (words >> 32).tolist()
     xcc = (words & 0xFFFFFFFF).tolist()
 
     def members(gi):
-        return [gi % 8 + 8 * ((gi // 8) * slices + k) for k in range(slices)]
+        if grid_groups % 8 == 0:
+            return [gi % 8 + 8 * ((gi // 8) * slices + k) for k in range(slices)]
+        return [gi * slices + k for k in range(slices)]
 
     real = sorted(b for gi in range(groups) for b in members(gi))
     assert len(set(real)) == groups * slices and max(real) < grid_groups * slices
@@ -647,7 +653,10 @@ def test_xcd_check_words_record_group_placement(gpu, hip_lib, B, H):
     on_one = [len({xcc[b] for b in members(gi)}) == 1 for gi in range(groups)]
     print(f"B={B} H={H} groups={groups} grid groups={grid_groups} slices={slices} "
           f"xcc of the first blocks {xcc[:16]} groups on one XCD: {sum(on_one)}/{groups}", flush=True)
-    assert all(on_one)
+    if padded:
+        assert all(on_one)
+    else:
+        assert not all(on_one)
 
 
 # ----------------------------------- module vs torch.nn.GRU on the GPU ---
