@@ -47,6 +47,13 @@ __device__ __forceinline__ int seg_map(const SegMap& s, int i) {
     return s.len ? (i / s.len) * s.stride + s.off + i % s.len : i;
 }
 
+__device__ __forceinline__ const float* uniform_ptr(const float* p) {
+    const unsigned long long v = reinterpret_cast<uintptr_t>(p);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return reinterpret_cast<const float*>(((unsigned long long)hi << 32) | lo);
+}
+
 template <int KMAJOR, bool SHIFT, bool SEG>
 __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, int k) {
     if constexpr (KMAJOR == 0) {
@@ -55,6 +62,15 @@ __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, i
         k = seg_map<SEG>(op.seg, k);
         if constexpr (SHIFT) {
             const int t = k % op.shift_T;
+            if constexpr (SEG) {
+                // The chunked products pick the base from the two pointers
+                // read as wave-uniform values: picking between the two fields
+                // made the compiler copy both into a private array indexed
+                // per lane (scratch loads).
+                const float* first = uniform_ptr(op.shift_first);
+                const float* rest = uniform_ptr(op.ptr);
+                return t == 0 ? first + (size_t)(k / op.shift_T) * op.ld + r : rest + (size_t)(k - 1) * op.ld + r;
+            }
             if (t == 0) return op.shift_first + (size_t)(k / op.shift_T) * op.ld + r;
             return op.ptr + (size_t)(k - 1) * op.ld + r;
         } else {
@@ -63,9 +79,34 @@ __device__ __forceinline__ const float* elem_ptr(const GemmOperand& op, int r, i
     }
 }
 
+// Raw buffer loads from a wave-uniform base.  The resource spans 2^31 bytes
+// and a lane given the offset kOffRange is outside it and reads zero (the
+// hardware's range check), so bounds-checked loads need no exec-mask
+// branches (behind which the compiler waited for each load before issuing
+// the next).  In-range offsets stay below 2^31 because leading dimensions are
+// below 2^22 floats (checked on the host).
+constexpr unsigned kOffRange = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t range_rsrc(const float* base) {
+    // word 3: the 32-bit data format (a zero format would read zero), no swizzle
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)kOffRange, 0x00020000);
+}
+__device__ __forceinline__ float load_in_range(const float* base, unsigned off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(range_rsrc(base), off, 0, 0));
+}
+typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load4_in_range(const float* base, unsigned off) {
+    // (the whole vector is cast: casting its elements one by one compiled to
+    // a single dword load)
+    const uintx4 u = __builtin_amdgcn_raw_buffer_load_b128(range_rsrc(base), off, 0, 0);
+    const floatx4 f = __builtin_bit_cast(floatx4, u);
+    return make_float4(f[0], f[1], f[2], f[3]);
+}
+
 // Register staging of one BMxBK operand tile (NV4 float4 per thread).
 // KMAJOR == 0: thread -> (row tid/KQ + (NT/KQ) i, k 4*(tid%KQ) .. +3), KQ = BK/4
 // KMAJOR == 1: thread -> (k tid/32 + (NT/32) i, row 4*(tid%32) .. +3)
+// In both, element group i starts at a wave-uniform row and k, and a lane's
+// offset from that start is the same for every i.
 constexpr int kDirectBK = 16;
 constexpr int kSplitBK = 16;
 static_assert(BM == 128 && BN == 128 && NT == 256, "tile staging layout");
@@ -105,6 +146,69 @@ __device__ __forceinline__ void load_tile(const GemmOperand& op, bool vec, int r
         }
         return;
     }
+    if (!vec) {
+        // Operands that are not float4-aligned: one float per lane, the lanes
+        // of a wave on consecutive addresses of the contiguous dimension.
+        // Element x = NT (4 i + c) + tid of the tile, held in component c of
+        // v[i], is row x % BM at k x / BM of a k-major tile (a wave reads 64
+        // rows of one k) and row x / BK at k x % BK of a row-major one (16 k
+        // of four rows).  store_tile writes it back in the same order.  (The
+        // float4 order below read four floats 16 bytes apart per lane:
+        // 2.3-3x slower GEMMs at hidden size 129.)
+        if constexpr (!SHIFT && !SEG) {
+            // Element x's address is a wave-uniform base (the element's row or
+            // k offset, x / NT, is the same in every lane) plus the lane's
+            // offset, which is the same for every element: one VGPR of
+            // addressing instead of eight 64-bit addresses per operand.
+            const int lr = KMAJOR == 1 ? tid % BM : tid / BK;  // lane's row in an element group
+            const int lk = KMAJOR == 1 ? tid / BM : tid % BK;  // lane's k in an element group
+            const unsigned lane_off = 4u * (KMAJOR == 1 ? lk * op.ld + lr : lr * op.ld + lk);
+#pragma unroll
+            for (int i = 0; i < NV4; ++i) {
+                float e[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int j = 4 * i + c;
+                    const int gr = KMAJOR == 1 ? r0 : r0 + (NT / BK) * j;  // group's first row
+                    const int gk = KMAJOR == 1 ? k0 + (NT / BM) * j : k0;  // group's first k
+                    const float* base = op.ptr + (KMAJOR == 1 ? (size_t)gk * op.ld + gr : (size_t)gr * op.ld + gk);
+                    const bool in = gr + lr < rows && gk + lk < kend;
+                    e[c] = load_in_range(base, in ? lane_off : kOffRange);
+                }
+                v[i] = make_float4(e[0], e[1], e[2], e[3]);
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < NV4; ++i) {
+            float e[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int x = (4 * i + c) * NT + tid;
+                const int r = r0 + (KMAJOR == 1 ? x % BM : x / BK);
+                const int k = k0 + (KMAJOR == 1 ? x / BM : x % BK);
+                e[c] = (r < rows && k < kend) ? *elem_ptr<KMAJOR, SHIFT, SEG>(op, r, k) : 0.f;
+            }
+            v[i] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+        return;
+    }
+    if constexpr (!SHIFT && !SEG) {
+        // edge tile of a vector-capable operand: a float4 is entirely in or
+        // out (the contiguous extent is a multiple of 4)
+        const int lr = KMAJOR == 0 ? tid / KQ : 4 * (tid % 32);
+        const int lk = KMAJOR == 0 ? 4 * (tid % KQ) : tid / 32;
+        const unsigned lane_off = 4u * (KMAJOR == 0 ? lr * op.ld + lk : lk * op.ld + lr);
+#pragma unroll
+        for (int i = 0; i < NV4; ++i) {
+            const int gr = KMAJOR == 0 ? r0 + (NT / KQ) * i : r0;
+            const int gk = KMAJOR == 0 ? k0 : k0 + (NT / 32) * i;
+            const float* base = op.ptr + (KMAJOR == 0 ? (size_t)gr * op.ld + gk : (size_t)gk * op.ld + gr);
+            const bool in = gr + lr < rows && gk + lk < kend;
+            v[i] = load4_in_range(base, in ? lane_off : kOffRange);
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
         int r, k;
@@ -115,22 +219,11 @@ __device__ __forceinline__ void load_tile(const GemmOperand& op, bool vec, int r
             k = k0 + tid / 32 + (NT / 32) * i;
             r = r0 + 4 * (tid % 32);
         }
-        if (vec) {
-            // The contiguous extent is a multiple of 4 and rows are 16-byte
-            // aligned, so a float4 is entirely in or out.
-            const bool in = (r < rows) && (k < kend);
-            v[i] = in ? *reinterpret_cast<const float4*>(elem_ptr<KMAJOR, SHIFT, SEG>(op, r, k))
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-        } else {
-            float e[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int rr = KMAJOR == 0 ? r : r + c;
-                const int kk = KMAJOR == 0 ? k + c : k;
-                e[c] = (rr < rows && kk < kend) ? *elem_ptr<KMAJOR, SHIFT, SEG>(op, rr, kk) : 0.f;
-            }
-            v[i] = make_float4(e[0], e[1], e[2], e[3]);
-        }
+        // The contiguous extent is a multiple of 4 and rows are 16-byte
+        // aligned, so a float4 is entirely in or out.
+        const bool in = (r < rows) && (k < kend);
+        v[i] = in ? *reinterpret_cast<const float4*>(elem_ptr<KMAJOR, SHIFT, SEG>(op, r, k))
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
@@ -147,8 +240,26 @@ constexpr int lds_tile_floats() {
 }
 
 template <int GK, int LF, int BK, int NV4 = BM * BK / (4 * NT), int KQ = BK / 4>
-__device__ __forceinline__ void store_tile(float* lds, int tid, const float4 (&v)[NV4]) {
+__device__ __forceinline__ void store_tile(float* lds, int tid, bool vec, const float4 (&v)[NV4]) {
     static_assert(!(GK == 1 && LF == 0), "k-major operands are staged in k form");
+    if (!vec) {
+        // the element order of load_tile's one-float-per-lane path
+#pragma unroll
+        for (int i = 0; i < NV4; ++i) {
+            const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int x = (4 * i + c) * NT + tid;
+                const int r = GK == 1 ? x % BM : x / BK;
+                const int k = GK == 1 ? x / BM : x % BK;
+                if constexpr (LF == 0)
+                    lds[r * (BK + 4) + k] = e[c];
+                else
+                    lds[k * LDSP + r] = e[c];
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
         if constexpr (GK == 0 && LF == 0) {
@@ -305,20 +416,24 @@ __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int l
 // k-tile is loaded into registers while the MFMAs of the current one run,
 // then stored to the other LDS buffer; one barrier per k-tile.  Interior
 // tiles of vector-capable operands load float4 without bounds checks; edge
-// tiles check per element.
-template <int AK, int BKM, bool BSHIFT, bool SEG, int BK>
+// tiles check per element.  UA: the kernel instance for products with an
+// operand that is not float4-aligned (a_vec / b_vec read at run time);
+// otherwise both operands take the float4 loads, and the one-float-per-lane
+// code, whose addresses would hold ~40 more VGPRs and cost the aligned
+// kernels their third workgroup per CU, is not compiled in.
+template <int AK, int BKM, bool BSHIFT, bool SEG, int BK, bool UA>
 __device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int nkb,
                                                  int tid, int lane, int wm, int wn, bool colsum, float& cs,
                                                  float* As0, float* As1, float* Bs0, float* Bs1,
                                                  floatx4 (&acc)[4][4]) {
     constexpr int NV4 = BM * BK / (4 * NT);
-    const bool av = p.a_vec != 0, bv = p.b_vec != 0;
+    const bool av = !UA || p.a_vec != 0, bv = !UA || p.b_vec != 0;
     float4 ra[NV4], rb[NV4];
     if (nkb > 0) {
         load_tile<AK, false, SEG, BK>(p.a, av, p.m, kend, m0, kbeg, tid, ra);
         load_tile<BKM, BSHIFT, SEG, BK>(p.b, bv, p.n, kend, n0, kbeg, tid, rb);
-        store_tile<AK, AK, BK>(As0, tid, ra);
-        store_tile<BKM, 1, BK>(Bs0, tid, rb);
+        store_tile<AK, AK, BK>(As0, tid, av, ra);
+        store_tile<BKM, 1, BK>(Bs0, tid, bv, rb);
     }
     __syncthreads();
     for (int kb = 0; kb < nkb; ++kb) {
@@ -333,8 +448,8 @@ __device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int 
         }
         mma_tile<AK, BK>(as, bs, lane, wm, wn, tid, colsum, cs, acc);
         if (more) {
-            store_tile<AK, AK, BK>(as_n, tid, ra);
-            store_tile<BKM, 1, BK>(bs_n, tid, rb);
+            store_tile<AK, AK, BK>(as_n, tid, av, ra);
+            store_tile<BKM, 1, BK>(bs_n, tid, bv, rb);
         }
         __syncthreads();
     }
@@ -527,7 +642,7 @@ __device__ __forceinline__ void store_c(const GemmArgs& p, int m0, int n0, int b
 }
 
 // One output tile (bx, by) of k-chunk bz.
-template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK>
+template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK, bool UA>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int bz, float* smem) {
     constexpr int AF = lds_tile_floats<AK, BK>();
     constexpr int BF = lds_tile_floats<1, BK>();
@@ -558,7 +673,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int
     if (kDma && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 && (kend - kbeg) % BK == 0)
         mainloop_dma<AK, BKM, BSHIFT, SEG>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, smem, acc);
     else
-        mainloop<AK, BKM, BSHIFT, SEG, BK>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
+        mainloop<AK, BKM, BSHIFT, SEG, BK, UA>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
                                            Bs1, acc);
     store_c<AK, SPLIT, SEG>(p, m0, n0, bz, wm, wn, lane, acc);
     if (colsum && tid < BM && m0 + tid < p.m) {
@@ -567,7 +682,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int
     }
 }
 
-template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, int BK = SPLIT ? kSplitBK : kDirectBK>
+template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG, bool UA, int BK = SPLIT ? kSplitBK : kDirectBK>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<AK, BK>()];
     int bx, by, bz = 0;
@@ -578,7 +693,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
         for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < p.zero_words; i += (size_t)gridDim.x * NT)
             p.zero[i] = 0ull;
     }
-    gemm_tile<AK, BKM, BSHIFT, SPLIT, SEG, BK>(p, bx, by, bz, smem);
+    gemm_tile<AK, BKM, BSHIFT, SPLIT, SEG, BK, UA>(p, bx, by, bz, smem);
 }
 
 // Two split-K products of k-major operands in one launch: workgroups
@@ -586,17 +701,17 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs p) {
 // gradients dW_hh, whose B operand is row-remapped, and dW_ih).  One launch
 // of both at half the slices each keeps three workgroups per CU with half
 // the partial sums and one ramp-up and tail instead of two.
-template <bool SHIFT0, bool SEG>
+template <bool SHIFT0, bool SEG, bool UA>
 __global__ __launch_bounds__(NT) void gemm_f32_pair_kernel(GemmArgs p0, GemmArgs p1) {
     __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<1, kSplitBK>()];
     const int blocks0 = p0.tiles * p0.ksplit;
     int bx, by, bz;
     if ((int)blockIdx.x < blocks0) {
         split_coords(p0, blockIdx.x, bx, by, bz);
-        gemm_tile<1, 1, SHIFT0, true, SEG, kSplitBK>(p0, bx, by, bz, smem);
+        gemm_tile<1, 1, SHIFT0, true, SEG, kSplitBK, UA>(p0, bx, by, bz, smem);
     } else {
         split_coords(p1, blockIdx.x - blocks0, bx, by, bz);
-        gemm_tile<1, 1, false, true, SEG, kSplitBK>(p1, bx, by, bz, smem);
+        gemm_tile<1, 1, false, true, SEG, kSplitBK, UA>(p1, bx, by, bz, smem);
     }
 }
 
@@ -809,7 +924,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceJob j0, Reduce
 // its weight-gradient reductions are independent: the reductions stream
 // partial sums from HBM while the product keeps the matrix cores busy, on
 // the workgroup slots the product's tiles leave free.
-template <int AK, int BKM>
+template <int AK, int BKM, bool UA>
 __global__ __launch_bounds__(NT) void gemm_direct_reduce_kernel(GemmArgs p, ReduceJob j0, ReduceJob j1) {
     static_assert(NT == 256, "reduction teams assume 256-thread workgroups");
     __shared__ __attribute__((aligned(16))) float smem[gemm_smem_floats<AK, kDirectBK>()];
@@ -819,7 +934,7 @@ __global__ __launch_bounds__(NT) void gemm_direct_reduce_kernel(GemmArgs p, Redu
     }
     int bx, by;
     direct_coords(p, blockIdx.x, bx, by);
-    gemm_tile<AK, BKM, false, false, false, kDirectBK>(p, bx, by, 0, smem);
+    gemm_tile<AK, BKM, false, false, false, kDirectBK, UA>(p, bx, by, 0, smem);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -833,6 +948,24 @@ bool vec_ok(const GemmOperand& op, int rows, int k) {
     return true;
 }
 
+// Leading dimensions are below 2^22 floats: the bounds-checked tile loads
+// address a lane's element (at most 63 ld + 15 floats from a wave-uniform
+// base) with a 32-bit byte offset below 2^31.
+int check_ld(const GemmOperand& a, const GemmOperand& b) {
+    constexpr int kMaxLd = 1 << 22;
+    if (a.ld < 0 || b.ld < 0 || a.ld >= kMaxLd || b.ld >= kMaxLd)
+        return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: leading dimensions must be below 2^22");
+    return 0;
+}
+
+template <int AK, int BKM, bool BSHIFT, bool SPLIT, bool SEG>
+void launch_gemm_kernel(const GemmArgs& args, dim3 grid, hipStream_t stream) {
+    if (args.a_vec && args.b_vec)
+        hipLaunchKernelGGL((gemm_f32_kernel<AK, BKM, BSHIFT, SPLIT, SEG, false>), grid, dim3(NT), 0, stream, args);
+    else
+        hipLaunchKernelGGL((gemm_f32_kernel<AK, BKM, BSHIFT, SPLIT, SEG, true>), grid, dim3(NT), 0, stream, args);
+}
+
 template <bool SPLIT, bool SEG>
 int launch_gemm_t(const GemmArgs& args, dim3 grid, hipStream_t stream) {
     const int ak = args.a.kmajor, bk = args.b.kmajor;
@@ -842,19 +975,19 @@ int launch_gemm_t(const GemmArgs& args, dim3 grid, hipStream_t stream) {
         // the weight gradients: both operands k-major
         if (!ak || !bk) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: split-K products take k-major operands");
         if (shift)
-            hipLaunchKernelGGL((gemm_f32_kernel<1, 1, true, true, SEG>), grid, dim3(NT), 0, stream, args);
+            launch_gemm_kernel<1, 1, true, true, SEG>(args, grid, stream);
         else
-            hipLaunchKernelGGL((gemm_f32_kernel<1, 1, false, true, SEG>), grid, dim3(NT), 0, stream, args);
+            launch_gemm_kernel<1, 1, false, true, SEG>(args, grid, stream);
     } else {
         if (shift) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: the row remap is for split-K products");
         if (!ak && !bk)
-            hipLaunchKernelGGL((gemm_f32_kernel<0, 0, false, false, SEG>), grid, dim3(NT), 0, stream, args);
+            launch_gemm_kernel<0, 0, false, false, SEG>(args, grid, stream);
         else if (!ak)
-            hipLaunchKernelGGL((gemm_f32_kernel<0, 1, false, false, SEG>), grid, dim3(NT), 0, stream, args);
+            launch_gemm_kernel<0, 1, false, false, SEG>(args, grid, stream);
         else if (!bk)
-            hipLaunchKernelGGL((gemm_f32_kernel<1, 0, false, false, SEG>), grid, dim3(NT), 0, stream, args);
+            launch_gemm_kernel<1, 0, false, false, SEG>(args, grid, stream);
         else
-            hipLaunchKernelGGL((gemm_f32_kernel<1, 1, false, false, SEG>), grid, dim3(NT), 0, stream, args);
+            launch_gemm_kernel<1, 1, false, false, SEG>(args, grid, stream);
     }
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
@@ -900,6 +1033,7 @@ int gemm_direct(int m, int n, int k, const GemmOperand& a, const GemmOperand& b,
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
     if (!a.ptr || !b.ptr || !c) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: null operand");
     if ((long long)((m + BM - 1) / BM) * ((n + BN - 1) / BN) > 0x7fffffff) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
+    RKA_RETURN_IF_ERR(check_ld(a, b));
     GemmArgs args{};
     args.a = a;
     args.b = b;
@@ -940,6 +1074,7 @@ int split_args(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, 
     if (ksplit < 1 || z_off < 0 || z_off + ksplit > ksplit_total)
         return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: bad split slices");
     if (!a.kmajor || !b.kmajor) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: split-K products take k-major operands");
+    RKA_RETURN_IF_ERR(check_ld(a, b));
     GemmArgs& args = *out;
     args = GemmArgs{};
     args.a = a;
@@ -1006,10 +1141,18 @@ int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hi
     RKA_RETURN_IF_ERR(try_big_pair(a0, a1, p0.b.shift_T > 0, stream, &launched));
     if (launched) return 0;
     const dim3 grid(a0.tiles * a0.ksplit + a1.tiles * a1.ksplit);
-    if (p0.b.shift_T > 0)
-        hipLaunchKernelGGL((gemm_f32_pair_kernel<true, false>), grid, dim3(NT), 0, stream, a0, a1);
-    else
-        hipLaunchKernelGGL((gemm_f32_pair_kernel<false, false>), grid, dim3(NT), 0, stream, a0, a1);
+    const bool ua = !(a0.a_vec && a0.b_vec && a1.a_vec && a1.b_vec);
+    if (p0.b.shift_T > 0) {
+        if (ua)
+            hipLaunchKernelGGL((gemm_f32_pair_kernel<true, false, true>), grid, dim3(NT), 0, stream, a0, a1);
+        else
+            hipLaunchKernelGGL((gemm_f32_pair_kernel<true, false, false>), grid, dim3(NT), 0, stream, a0, a1);
+    } else {
+        if (ua)
+            hipLaunchKernelGGL((gemm_f32_pair_kernel<false, false, true>), grid, dim3(NT), 0, stream, a0, a1);
+        else
+            hipLaunchKernelGGL((gemm_f32_pair_kernel<false, false, false>), grid, dim3(NT), 0, stream, a0, a1);
+    }
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
 }
@@ -1053,10 +1196,22 @@ int splitk_reduce_pair(const SplitProduct& p0, const SplitProduct& p1, hipStream
     return launch_reduce(reduce_job(p0), reduce_job(p1), stream);
 }
 
+namespace {
+template <int AK, int BKM>
+void launch_direct_reduce(const GemmArgs& args, const ReduceJob& j0, const ReduceJob& j1, dim3 grid,
+                          hipStream_t stream) {
+    if (args.a_vec && args.b_vec)
+        hipLaunchKernelGGL((gemm_direct_reduce_kernel<AK, BKM, false>), grid, dim3(NT), 0, stream, args, j0, j1);
+    else
+        hipLaunchKernelGGL((gemm_direct_reduce_kernel<AK, BKM, true>), grid, dim3(NT), 0, stream, args, j0, j1);
+}
+}  // namespace
+
 int gemm_direct_reduce_pair(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, float* c, int ldc,
                             const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream) {
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
     if (!a.ptr || !b.ptr || !c) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: null operand");
+    RKA_RETURN_IF_ERR(check_ld(a, b));
     if (a.seg.len || b.seg.len || b.shift_T > 0) {
         RKA_RETURN_IF_ERR(splitk_reduce_pair(p0, p1, stream));
         return gemm_direct(m, n, k, a, b, nullptr, c, ldc, stream);
@@ -1081,13 +1236,13 @@ int gemm_direct_reduce_pair(int m, int n, int k, const GemmOperand& a, const Gem
     const dim3 grid((unsigned)(args.tiles + reducers));
     const ReduceJob j0 = reduce_job(p0), j1 = reduce_job(p1);
     if (!a.kmajor && !b.kmajor)
-        hipLaunchKernelGGL((gemm_direct_reduce_kernel<0, 0>), grid, dim3(NT), 0, stream, args, j0, j1);
+        launch_direct_reduce<0, 0>(args, j0, j1, grid, stream);
     else if (!a.kmajor)
-        hipLaunchKernelGGL((gemm_direct_reduce_kernel<0, 1>), grid, dim3(NT), 0, stream, args, j0, j1);
+        launch_direct_reduce<0, 1>(args, j0, j1, grid, stream);
     else if (!b.kmajor)
-        hipLaunchKernelGGL((gemm_direct_reduce_kernel<1, 0>), grid, dim3(NT), 0, stream, args, j0, j1);
+        launch_direct_reduce<1, 0>(args, j0, j1, grid, stream);
     else
-        hipLaunchKernelGGL((gemm_direct_reduce_kernel<1, 1>), grid, dim3(NT), 0, stream, args, j0, j1);
+        launch_direct_reduce<1, 1>(args, j0, j1, grid, stream);
     RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
 }

@@ -138,6 +138,54 @@ def test_gemm_unaligned_operands_use_scalar_path(gpu, hip_lib):
     assert (c[:, :n].double().cpu() - ref).abs().max().item() < 1e-4
 
 
+# extents that are multiples of 4 (so the aligned storage takes the float4
+# paths), with edge tiles along m and n, k-tails and, at m = 1000, eight row
+# panels
+UNALIGNED_SHAPES = [(300, 200, 52), (132, 388, 132), (1000, 392, 72), (256, 256, 64)]
+
+
+@pytest.mark.parametrize("m,n,k", UNALIGNED_SHAPES)
+@pytest.mark.parametrize("a_kmajor,b_kmajor", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_unaligned_storage_matches_aligned_bitwise(gpu, hip_lib, m, n, k, a_kmajor, b_kmajor):
+    """An operand whose leading dimension is odd and whose base is one float
+    past a 16-byte boundary is staged one float per lane; the values land in
+    the same LDS places and meet the MFMAs in the same order as the float4
+    paths', so the product equals that of the same matrices in aligned
+    storage bit for bit (either operand unaligned, or both)."""
+    from rnn_kernel_amd import _lib
+
+    print(f"gemm storage m={m} n={n} k={k} a_kmajor={a_kmajor} b_kmajor={b_kmajor}", flush=True)
+    g = torch.Generator().manual_seed(m + 5 * n + 11 * k)
+    A = torch.randn(m, k, generator=g)
+    Bm = torch.randn(n, k, generator=g)
+    bias = torch.randn(n, generator=g).to(gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def stored(M, kmajor, unaligned):
+        """(buffer, byte offset, leading dimension) of M [rows, k] in the given layout."""
+        S = (M.T if kmajor else M).contiguous()
+        ld = S.shape[1] + (1 if unaligned else 0)
+        buf = torch.zeros(S.shape[0] * ld + 8, device=gpu)
+        off = 1 if unaligned else 0
+        buf[off:off + S.shape[0] * ld].view(S.shape[0], ld)[:, :S.shape[1]] = S.to(gpu)
+        return buf, 4 * off, ld
+
+    outs = {}
+    for ua_a, ua_b in [(0, 0), (1, 0), (0, 1), (1, 1)]:
+        a_buf, a_off, lda = stored(A, a_kmajor, ua_a)
+        b_buf, b_off, ldb = stored(Bm, b_kmajor, ua_b)
+        c = torch.full((m, n), float("nan"), device=gpu)
+        rc = hip_lib.rka_gemm_f32(m, n, k, a_buf.data_ptr() + a_off, lda, a_kmajor, b_buf.data_ptr() + b_off, ldb,
+                                  b_kmajor, bias.data_ptr(), c.data_ptr(), n, stream)
+        _lib.check(rc, "rka_gemm_f32")
+        outs[(ua_a, ua_b)] = c
+    torch.cuda.synchronize()
+    ref = A.double() @ Bm.double().T + bias.double().cpu()
+    assert (outs[(0, 0)].double().cpu() - ref).abs().max().item() <= 1e-6 * k + 1e-5
+    for key, c in outs.items():
+        assert torch.equal(c, outs[(0, 0)]), key
+
+
 # ------------------------------------------------- gate nonlinearities ---
 def test_gate_functions_accuracy_against_float64(gpu, hip_lib):
     """The recurrence kernels evaluate sigmoid / tanh from their definitions on
