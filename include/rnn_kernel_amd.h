@@ -105,6 +105,10 @@ int rka_gru_backward(const float* x, const float* h0,
 /* C[m,n] = sum_k A(m,k) B(n,k) (+ bias[n] if bias != NULL), fp32 MFMA.
  * A(m,k) = a[m*lda+k] if a_kmajor == 0 else a[k*lda+m];
  * B(n,k) = b[n*ldb+k] if b_kmajor == 0 else b[k*ldb+n].
+ * Any alignment and leading dimension below 2^22 (else
+ * RKA_ERR_UNSUPPORTED_SHAPE, nothing launched); operands whose contiguous
+ * extent, leading dimension and base are multiples of 16 bytes take the
+ * faster float4 paths, the others give the same results bit for bit.
  * Replaces the torch F.linear / matmul calls of gru.py:519-523,571-578. */
 int rka_gemm_f32(int m, int n, int k,
                  const float* a, int lda, int a_kmajor,

@@ -138,6 +138,21 @@ def test_gemm_unaligned_operands_use_scalar_path(gpu, hip_lib):
     assert (c[:, :n].double().cpu() - ref).abs().max().item() < 1e-4
 
 
+def test_gemm_rejects_leading_dimensions_from_2_pow_22(gpu, hip_lib):
+    """The tile loads form 32-bit offsets from a wave-uniform base, which holds
+    for leading dimensions below 2^22 floats; larger ones are refused before
+    anything is launched (the buffers here are far smaller than such a
+    leading dimension would imply, and are never read)."""
+    a = torch.zeros(64, device=gpu)
+    c = torch.zeros(16, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+    for lda, ldb in [(1 << 22, 4), (4, 1 << 22), (-1, 4)]:
+        rc = hip_lib.rka_gemm_f32(4, 4, 4, a.data_ptr(), lda, 0, a.data_ptr(), ldb, 0, None, c.data_ptr(), 4, stream)
+        assert rc == 1004, (lda, ldb, rc)
+    torch.cuda.synchronize()
+    assert torch.equal(c, torch.zeros_like(c))
+
+
 # extents that are multiples of 4 (so the aligned storage takes the float4
 # paths), with edge tiles along m and n, k-tails and, at m = 1000, eight row
 # panels
