@@ -296,6 +296,7 @@ struct GemmArgs {
     SegMap c_seg;          // direct mode: output row map
     unsigned long long* zero;  // direct mode: words cleared on the side (nullable)
     size_t zero_words;
+    int narrow;            // last columns left to gemm_narrow_kernel (0: none)
 };
 
 // Split mode runs a 1-D grid of tiles * ksplit workgroups.  Workgroups are
@@ -937,6 +938,86 @@ __global__ __launch_bounds__(NT) void gemm_direct_reduce_kernel(GemmArgs p, Redu
     gemm_tile<AK, BKM, false, false, false, kDirectBK, UA>(p, bx, by, 0, smem);
 }
 
+// ------------------------------------------------- narrow last columns ---
+// A split-K product whose n is whole 128-column panels plus w <= kNarrowMax
+// columns (the weight gradients at odd hidden sizes: n = H = 129) runs its
+// tiles over the panels only: a tile for the last w columns would spend 128
+// columns of MFMA work on w.  Those columns are summed here on the VALU, in
+// a fixed order (deterministic, though not bitwise a tile's sums).  A block
+// is 64 rows and four wavefronts.  Per 256-deep k slab, wavefront q sums k in
+// [64q, 64q + 64) of it for its 64 rows: lanes are rows, so each k is one
+// coalesced row segment of the k-major A.  At the end the four partial
+// sums are added in the order q = 0..3, and each k-chunk's sums go into the
+// product's partial buffer, which the reduction adds in the same fixed order
+// as the tiles' partials.  Blocks [0, blocks0) take p0, the rest p1 (the
+// weight-gradient pair).  The same summation for the direct products' last
+// columns, run after their tiles, measured slower than the edge tiles it
+// replaced (dx at hidden size 129: 101 vs 85 us).
+constexpr int kNarrowMax = 8;
+constexpr int kNarrowSlab = 256;  // k per LDS slab
+
+template <bool BSHIFT>
+__device__ __forceinline__ void narrow_block(const GemmArgs& p, int id, float* lds) {
+    float (*bs)[kNarrowMax] = reinterpret_cast<float (*)[kNarrowMax]>(lds);  // [kNarrowSlab][8]
+    float* part = lds + kNarrowSlab * kNarrowMax;                            // [4][64][8]
+    const int n0 = p.n - p.narrow;
+    const int mblocks = (p.m + 63) / 64;
+    const int mb = id % mblocks, z = id / mblocks;
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int m = mb * 64 + lane;
+    const int kbeg = z * p.kchunk;
+    const int kend = min(p.k, kbeg + p.kchunk);
+    float acc[kNarrowMax];
+#pragma unroll
+    for (int j = 0; j < kNarrowMax; ++j) acc[j] = 0.f;
+    for (int k0 = kbeg; k0 < kend; k0 += kNarrowSlab) {
+        for (int i = threadIdx.x; i < kNarrowSlab * kNarrowMax; i += 256) {
+            const int kk = i / kNarrowMax, j = i % kNarrowMax;
+            const int k = k0 + kk;
+            bs[kk][j] = (j < p.narrow && k < kend) ? *elem_ptr<1, BSHIFT, false>(p.b, n0 + j, k) : 0.f;
+        }
+        __syncthreads();
+        const int kq = k0 + 64 * q;
+        const int kn = max(0, min(64, kend - kq));
+        if (m < p.m) {
+            const float* a = p.a.ptr + (size_t)kq * p.a.ld + m;
+#pragma unroll 8
+            for (int kk = 0; kk < kn; ++kk) {
+                const float av = a[(size_t)kk * p.a.ld];
+#pragma unroll
+                for (int j = 0; j < kNarrowMax; ++j) acc[j] = fmaf(av, bs[64 * q + kk][j], acc[j]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < kNarrowMax; ++j) part[(q * 64 + lane) * kNarrowMax + j] = acc[j];
+    __syncthreads();
+    if (q != 0 || m >= p.m) return;
+#pragma unroll
+    for (int j = 0; j < kNarrowMax; ++j) {
+        if (j < p.narrow) {
+            float v = part[lane * kNarrowMax + j];
+            v += part[(64 + lane) * kNarrowMax + j];
+            v += part[(128 + lane) * kNarrowMax + j];
+            v += part[(192 + lane) * kNarrowMax + j];
+            p.partial[((size_t)(p.z_off + z) * p.m + m) * p.n + n0 + j] = v;
+        }
+    }
+}
+
+constexpr int kNarrowSmemBytes = (kNarrowSlab + 4 * 64) * kNarrowMax * (int)sizeof(float);
+
+template <bool BSHIFT0>
+__global__ __launch_bounds__(256) void gemm_narrow_kernel(GemmArgs p0, GemmArgs p1, int blocks0) {
+    __shared__ __attribute__((aligned(16))) float smem[kNarrowSmemBytes / sizeof(float)];
+    const int id = (int)blockIdx.x;
+    if (id < blocks0)
+        narrow_block<BSHIFT0>(p0, id, smem);
+    else
+        narrow_block<false>(p1, id - blocks0, smem);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // A float4 along the contiguous dimension is valid when that dimension's
@@ -955,6 +1036,30 @@ int check_ld(const GemmOperand& a, const GemmOperand& b) {
     constexpr int kMaxLd = 1 << 22;
     if (a.ld < 0 || b.ld < 0 || a.ld >= kMaxLd || b.ld >= kMaxLd)
         return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: leading dimensions must be below 2^22");
+    return 0;
+}
+
+// Columns of a split-K product past its last whole 128-column panel that
+// gemm_narrow_kernel takes instead of a tile (0: the tiles take every column).
+int narrow_cols(int n) {
+    const int r = n % BN;
+    return n > BN && r > 0 && r <= kNarrowMax ? r : 0;
+}
+
+// The narrow columns of the weight-gradient pair (after the tiles' launch).
+int launch_narrow_pair(const GemmArgs& p0, const GemmArgs& p1, bool shift0, hipStream_t stream) {
+    auto blocks = [](const GemmArgs& p) -> long long {
+        return p.narrow ? (long long)((p.m + 63) / 64) * p.ksplit : 0;
+    };
+    const long long b0 = blocks(p0), b1 = blocks(p1);
+    if (b0 + b1 == 0) return 0;
+    if (b0 + b1 > 0x7fffffff) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "gemm: grid too large");
+    const dim3 grid((unsigned)(b0 + b1));
+    if (shift0)
+        hipLaunchKernelGGL((gemm_narrow_kernel<true>), grid, dim3(256), 0, stream, p0, p1, (int)b0);
+    else
+        hipLaunchKernelGGL((gemm_narrow_kernel<false>), grid, dim3(256), 0, stream, p0, p1, (int)b0);
+    RKA_RETURN_IF_HIP(hipGetLastError());
     return 0;
 }
 
@@ -995,7 +1100,7 @@ int launch_gemm_t(const GemmArgs& args, dim3 grid, hipStream_t stream) {
 
 template <bool SPLIT>
 void finish_args(GemmArgs& args, int ksplit, bool av, bool bv) {
-    const int tm = (args.m + BM - 1) / BM, tn = (args.n + BN - 1) / BN;
+    const int tm = (args.m + BM - 1) / BM, tn = (args.n - args.narrow + BN - 1) / BN;
     args.tiles_m = tm;
     args.tiles = tm * tn;
     args.ksplit = ksplit;
@@ -1056,7 +1161,7 @@ size_t splitk_partial_floats(int m, int n, int ksplit) {
 }
 
 int choose_ksplit(int m, int n, int k, int num_cus, int wgs_per_cu) {
-    const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    const int tiles = ((m + BM - 1) / BM) * ((n - narrow_cols(n) + BN - 1) / BN);
     const int target = wgs_per_cu > 0 ? wgs_per_cu * (num_cus > 0 ? num_cus : 256) : (num_cus > 0 ? num_cus : 256) / 2;
     int ks = (target + tiles - 1) / tiles;
     const int max_by_k = k / (8 * kSplitBK);  // at least 8 tiles of k per split
@@ -1069,7 +1174,7 @@ int choose_ksplit(int m, int n, int k, int num_cus, int wgs_per_cu) {
 
 namespace {
 int split_args(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum, float* partial,
-               int ksplit, int z_off, int ksplit_total, GemmArgs* out) {
+               int ksplit, int z_off, int ksplit_total, bool narrow, GemmArgs* out) {
     if (m <= 0 || n <= 0 || k < 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: m and n must be positive");
     if (ksplit < 1 || z_off < 0 || z_off + ksplit > ksplit_total)
         return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: bad split slices");
@@ -1089,6 +1194,7 @@ int split_args(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, 
     args.want_colsum = want_colsum ? 1 : 0;
     args.z_off = z_off;
     args.ksplit_total = ksplit_total;
+    args.narrow = narrow ? narrow_cols(n) : 0;
     finish_args<true>(args, ksplit, vec_ok(a, m, k), vec_ok(b, n, k));
     return 0;
 }
@@ -1124,16 +1230,16 @@ int try_big_pair(GemmArgs a0, GemmArgs a1, bool shift0, hipStream_t stream, bool
 int gemm_splitk_partials(int m, int n, int k, const GemmOperand& a, const GemmOperand& b, bool want_colsum,
                          float* partial, int ksplit, int z_off, int ksplit_total, hipStream_t stream) {
     GemmArgs args;
-    RKA_RETURN_IF_ERR(split_args(m, n, k, a, b, want_colsum, partial, ksplit, z_off, ksplit_total, &args));
+    RKA_RETURN_IF_ERR(split_args(m, n, k, a, b, want_colsum, partial, ksplit, z_off, ksplit_total, false, &args));
     return launch_gemm<true>(args, ksplit, args.a_vec != 0, args.b_vec != 0, stream);
 }
 
 int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hipStream_t stream) {
     GemmArgs a0, a1;
     RKA_RETURN_IF_ERR(split_args(p0.m, p0.n, p0.k, p0.a, p0.b, p0.colsum != nullptr, p0.partial, p0.ksplit, 0,
-                                 p0.ksplit, &a0));
+                                 p0.ksplit, true, &a0));
     RKA_RETURN_IF_ERR(split_args(p1.m, p1.n, p1.k, p1.a, p1.b, p1.colsum != nullptr, p1.partial, p1.ksplit, 0,
-                                 p1.ksplit, &a1));
+                                 p1.ksplit, true, &a1));
     if (p1.b.shift_T > 0) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: only the first product of a pair is remapped");
     const bool seg = a0.a.seg.len || a0.b.seg.len || a1.a.seg.len || a1.b.seg.len;
     if (seg) return fail(RKA_ERR_INVALID_ARGUMENT, "gemm: pair products take whole operands");
@@ -1154,7 +1260,7 @@ int gemm_splitk_pair_partials(const SplitProduct& p0, const SplitProduct& p1, hi
             hipLaunchKernelGGL((gemm_f32_pair_kernel<false, false, false>), grid, dim3(NT), 0, stream, a0, a1);
     }
     RKA_RETURN_IF_HIP(hipGetLastError());
-    return 0;
+    return launch_narrow_pair(a0, a1, p0.b.shift_T > 0, stream);
 }
 
 namespace {

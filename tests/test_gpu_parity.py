@@ -244,6 +244,9 @@ LAYER_SHAPES = [
     (130, 4, 6, 130),    # three slices, two rows per workgroup
     (400, 5, 4, 160),    # three slices at four rows not resident: batch-slice launches of 80 groups
     (1, 3, 4, 768),      # the largest hidden size at one batch row (LDS-tiled, one unit per workgroup)
+    (8, 512, 135, 133),  # weight gradients' last 5 (dW_hh) / 7 (dW_ih) columns summed apart from the tiles,
+                         # k = B T = 4096 in 32 chunks (c3 at H = 129, 130 runs chunks of two 256-deep slabs)
+    (2, 70, 136, 136),   # ... 8 columns each, k = 140: one chunk ending inside its slab
 ]
 
 
