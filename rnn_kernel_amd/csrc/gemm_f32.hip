@@ -9,18 +9,21 @@
 // blocks; three workgroups per CU.  Interior tiles load their 16-deep
 // operand tiles straight from global memory into a three-stage LDS ring
 // (global_load_lds_dwordx4); edge tiles and operands that are not 16-byte
-// aligned stage them through registers into double-buffered LDS.  The LDS
+// aligned stage them through registers into double-buffered LDS (bounds-
+// checked loads as range-checked buffer loads; unaligned operands one float
+// per lane, in kernel instances of their own).  The LDS
 // forms are chosen so that every MFMA operand read is one conflict-free
 // ds_read_b128 feeding four MFMAs: a k-major tile is kept [k][row] (a lane
 // reads four rows at one k), a row-major one [row][k] (four k of one row;
 // swizzled in the ring, padded in the register path), and a lane's four B
 // blocks are four adjacent output columns, stored as one float4 (a
 // streaming store for the direct products).  At c2 inside the training
-// step: input projection 121 us, dx 110 us, the dW pair 243 us.  Each
-// operand layout is a template instance, so no product carries another's
-// address arithmetic.  The weight gradients (K = B*T rows) use
-// split-K with a fixed-order reduction, so results are deterministic run to
-// run.
+// step: input projection 119 us, dx with the weight-gradient reductions
+// 110 us, the dW pair (192x256 tiles) 233 us.  Each operand layout is a
+// template instance, so no product carries another's address arithmetic.
+// The weight gradients (K = B*T rows) use split-K with a fixed-order
+// reduction, so results are deterministic run to run; up to 8 columns past
+// their last 128-column panel are summed on the VALU instead of in a tile.
 #include <atomic>
 
 #include "rka_internal.h"
