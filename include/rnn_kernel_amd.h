@@ -133,9 +133,11 @@ int rka_gru_recurrence_forward(const float* gx, const float* h0,
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  No counterpart in the
  * reference.  The exchange state lives in a static device array of the
- * library, one per GPU (4 MiB + 32 KiB + 256 B, held until the process
- * ends; set up on the first call on each device); the call allocates no
- * device memory.  Limit: batch * hidden_size <= 262144 (2 B H 8-byte
+ * library (4 MiB + 32 KiB + 256 B): it is part of the library's code
+ * object, so every process that loads the library holds it on each device
+ * the code object is loaded on, until the process ends, whether or not it
+ * calls this entry point; the first call on a device only looks up its
+ * address there.  The call allocates no device memory.  Limit: batch * hidden_size <= 262144 (2 B H 8-byte
  * words in 4 MiB); larger shapes return RKA_ERR_UNSUPPORTED_SHAPE without
  * launching.  Every call on a GPU shares that GPU's array: calls that
  * overlap on one GPU (different streams or threads without ordering) race
@@ -172,21 +174,6 @@ int rka_gru_recurrence_backward(const float* dy, const float* dhn,
 #define RKA_GEMM_TILES_AUTO 0
 #define RKA_GEMM_TILES_128 1
 int rka_set_gemm_tiles(int mode);
-
-/* Number of time chunks the backward of a layer runs in (0 = automatic,
- * currently 1; at most 8, and never more than seq_len).  With several chunks
- * the backward recurrence is launched once per time range, latest first,
- * and the gradient GEMMs of each finished range run on a second stream
- * concurrently with the next range (slower on MI355X at the benchmark
- * shape, hence not automatic).  Affects later calls on all threads and the
- * backward workspace size.  No counterpart in the reference (its backward is
- * one launch, src/rnn_kernel/a100/prod/gru.py:531-580); exported for tests
- * and tuning. */
-int rka_set_backward_chunks(int chunks);
-
-/* Chunks rka_gru_backward uses for seq_len under the current setting
- * (-1 on bad arguments). */
-int rka_backward_chunks(int seq_len);
 
 /* Poll rounds a recurrence kernel's wait for another workgroup's words
  * makes before it gives up (0 = the default, 2^24 rounds, about 2 s at the
@@ -248,26 +235,21 @@ int rka_recurrence_abort_count(unsigned long long* count);
  *         0 = auto), param = wavefronts holding (row, unit) pairs (1, 2, 4,
  *         0 = auto);
  * kind 2: register-resident; units = 64 (or 0), param = batch rows per
- *         workgroup (1, 2, 4, 0 = auto);
- * kind 3: matrix-core forward (dir 0 only): 16 batch rows x 16 hidden units
- *         per workgroup on v_mfma_f32_16x16x4_f32; batch a multiple of 16,
- *         hidden_size a multiple of 32 up to 256 (units and param 0).  Never
- *         chosen automatically: measured slower than the register kernel at
- *         every batch tried (2.31 vs 2.11 us per step at B = 256, H = 256). */
+ *         workgroup (1, 2, 4, 0 = auto). */
 #define RKA_REC_AUTO 0
 #define RKA_REC_TILED 1
 #define RKA_REC_REGISTER 2
-#define RKA_REC_MFMA 3
 int rka_set_recurrence_config(int dir, int kind, int units, int param);
 
 /* Describe the decomposition the next recurrence call would use for this
- * shape: writes {kind, groups (per launch), slices, units, rows_per_group,
- * pair_waves, chunk, lds_bytes, launches, batch_per_launch}.  A batch whose
- * grid would not be resident on an idle GPU runs as `launches` launches
- * over consecutive slices of batch_per_launch rows, each grid resident (the
- * reference refuses such a batch instead, src/rnn_kernel/a100/prod/gru.py:257-263). */
-int rka_describe_recurrence(int dir, int batch, int hidden_size, int out10[10]);
-
+ * shape: writes the first min(n_out, 10) of {kind, groups (per launch),
+ * slices, units, rows_per_group, pair_waves, chunk, lds_bytes, launches,
+ * batch_per_launch} to out and returns 0 (n_out < 1 is an error).  A batch
+ * whose grid would not be resident on an idle GPU runs as `launches`
+ * launches over consecutive slices of batch_per_launch rows, each grid
+ * resident (the reference refuses such a batch instead,
+ * src/rnn_kernel/a100/prod/gru.py:257-263). */
+int rka_describe_recurrence(int dir, int batch, int hidden_size, int* out, int n_out);
 
 /* Evaluates the recurrence kernels' gate nonlinearities (the same device
  * functions) elementwise: sigmoid_out = sigmoid(x), tanh_out = tanh(x).
@@ -281,11 +263,10 @@ int rka_eval_gate_functions(const float* x, float* sigmoid_out, float* tanh_out,
  * its stream; rka_profile_read() waits for the recorded events, returns the
  * summed milliseconds and launch counts per stage and clears the records.
  * Stage ids: 0 input GEMM, 1 forward recurrence, 2 backward recurrence,
- * 3 dW_hh and dW_ih split-K products (one launch unless the backward runs
- * in time chunks), 4 their split-K reductions into dW and db, 5 dx GEMM.
- * When dx is requested from an unchunked backward, the reductions run in
- * the dx GEMM's launch and are reported under stage 5 (stage 4 then has no
- * launches).
+ * 3 dW_hh and dW_ih split-K products (one launch), 4 their split-K
+ * reductions into dW and db, 5 dx GEMM.  When dx is requested, the
+ * reductions run in the dx GEMM's launch and are reported under stage 5
+ * (stage 4 then has no launches).
  */
 #define RKA_NUM_STAGES 6
 int rka_profile_enable(int on);

@@ -34,14 +34,12 @@ SIGNATURES = {
     "rka_gru_recurrence_forward_noalloc": (_I, [_P] * 7 + [_I, _I, _I, _P]),
     "rka_gru_recurrence_backward": (_I, [_P] * 8 + [_P, _SZ, _I, _I, _I, _P]),
     "rka_set_recurrence_config": (_I, [_I, _I, _I, _I]),
-    "rka_set_backward_chunks": (_I, [_I]),
     "rka_set_spin_limit": (_I, [_I]),
     "rka_set_gemm_tiles": (_I, [_I]),
     "rka_set_exchange_stores": (_I, [_I]),
     "rka_recurrence_abort_count": (_I, [ctypes.POINTER(ctypes.c_ulonglong)]),
     "rka_set_stall_block": (_I, [_I]),
-    "rka_backward_chunks": (_I, [_I]),
-    "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I)]),
+    "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I), _I]),
     "rka_eval_gate_functions": (_I, [_P, _P, _P, _I, _P]),
     "rka_profile_enable": (_I, [_I]),
     "rka_profile_read": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
@@ -117,13 +115,13 @@ def profile_read() -> dict:
     return {lib.rka_profile_stage_name(i).decode(): (ms[i], cnt[i]) for i in range(NUM_STAGES)}
 
 
-REC_KINDS = {0: "auto", 1: "tiled", 2: "register", 3: "mfma"}
+REC_KINDS = {0: "auto", 1: "tiled", 2: "register"}
 
 
 def describe_recurrence(direction: int, batch: int, hidden: int) -> dict:
     """Decomposition the next recurrence call would use (0 forward, 1 backward)."""
     out = (ctypes.c_int * 10)()
-    check(load().rka_describe_recurrence(direction, batch, hidden, out), "rka_describe_recurrence")
+    check(load().rka_describe_recurrence(direction, batch, hidden, out, 10), "rka_describe_recurrence")
     keys = ("kind", "groups", "slices", "units", "rows", "pair_waves", "chunk", "lds_bytes", "launches",
             "batch_per_launch")
     d = dict(zip(keys, list(out)))
@@ -133,11 +131,6 @@ def describe_recurrence(direction: int, batch: int, hidden: int) -> dict:
 
 def set_recurrence_config(direction: int, kind: int = 0, units: int = 0, param: int = 0) -> None:
     check(load().rka_set_recurrence_config(direction, kind, units, param), "rka_set_recurrence_config")
-
-
-def set_backward_chunks(chunks: int) -> None:
-    """Time chunks of the backward (0 = automatic); see rka_set_backward_chunks."""
-    check(load().rka_set_backward_chunks(chunks), "rka_set_backward_chunks")
 
 
 def set_spin_limit(polls: int) -> None:
@@ -171,6 +164,3 @@ def recurrence_abort_count() -> int:
     check(load().rka_recurrence_abort_count(ctypes.byref(n)), "rka_recurrence_abort_count")
     return int(n.value)
 
-
-def backward_chunks(seq_len: int) -> int:
-    return int(load().rka_backward_chunks(seq_len))

@@ -266,10 +266,12 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
     }
 
     // the owner lane's word in the slot of each step parity, as 32-bit
-    // offsets (2 B H < 2^31); the failure injection swaps the two
+    // unsigned offsets (2 B H < 2^32: the host keeps B H < 2^29); the
+    // failure injection swaps the two
     const int pub_flip = (int)blockIdx.x == p.stall_block ? 1 : 0;
-    const unsigned pub_off[2] = {(unsigned)(pub_flip * B * H + orow * H + u),
-                                 (unsigned)((1 - pub_flip) * B * H + orow * H + u)};
+    const unsigned slot_words = (unsigned)B * (unsigned)H, my_word = (unsigned)orow * (unsigned)H + (unsigned)u;
+    const unsigned pub_off[2] = {(unsigned)pub_flip * slot_words + my_word,
+                                 (unsigned)(1 - pub_flip) * slot_words + my_word};
     // outputs of the previous step, stored after the next poll
     float o_h = 0.f, o_r = 0.f, o_z = 0.f, o_n = 0.f, o_a = 0.f;
     float* y_row = y + (size_t)orow * T * H + u;
@@ -635,10 +637,12 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     // wave r < R owns row row0 + r: its pointwise math, G stores and words
     const int orow = row0 + (wave < R ? wave : 0);
     // the owner lane's first word in the slot of each step parity (32-bit
-    // offsets, 6 B H < 2^31); the failure injection swaps the two
+    // unsigned offsets, 6 B H < 2^32: the host keeps B H < 2^29); the
+    // failure injection swaps the two
     const int pub_flip = (int)blockIdx.x == p.stall_block ? 1 : 0;
-    const unsigned pub_off[2] = {(unsigned)(pub_flip * B * H3 + orow * H3 + u),
-                                 (unsigned)((1 - pub_flip) * B * H3 + orow * H3 + u)};
+    const unsigned slot_words = (unsigned)B * (unsigned)H3, my_word = (unsigned)orow * (unsigned)H3 + (unsigned)u;
+    const unsigned pub_off[2] = {(unsigned)pub_flip * slot_words + my_word,
+                                 (unsigned)(1 - pub_flip) * slot_words + my_word};
     const bool owner = wave < R && uvalid && orow < B;
     float dh = 0.f, ddirect = 0.f;
     float o_dan = 0.f, o_drh = 0.f, o_dzh = 0.f, o_dnh = 0.f;

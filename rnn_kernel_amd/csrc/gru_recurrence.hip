@@ -90,7 +90,6 @@ int choose_rec_config(int dir, int batch, int hidden, const DeviceInfo& dev, Rec
     }
     if (o.kind == REC_TILED) return tiled_choose(dir, batch, hidden, dev, o.units, o.param, cfg);
     if (o.kind == REC_REGISTER) return reg_choose(dir, batch, hidden, dev, o.units, o.param, cfg);
-    if (o.kind == REC_MFMA) return mfma_choose(dir, batch, hidden, dev, cfg);
     if (hidden <= 256 && reg_choose(dir, batch, hidden, dev, 0, 0, cfg) == 0) {
         clear_error();
         return 0;
@@ -161,8 +160,6 @@ int launch_slices(int dir, const RecConfig& c, rec::Args a, unsigned long long* 
         s.xcc_tag = (unsigned)((size_t)(T - a.t_end) * c.launches + k + 1);
         if (cs.kind == REC_REGISTER) {
             RKA_RETURN_IF_ERR(reg_launch(dir, cs, s, stream));
-        } else if (cs.kind == REC_MFMA) {
-            RKA_RETURN_IF_ERR(mfma_launch(dir, cs, s, stream));
         } else {
             RKA_RETURN_IF_ERR(tiled_launch(dir, cs, s, stream));
         }

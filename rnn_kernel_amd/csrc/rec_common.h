@@ -311,10 +311,4 @@ int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t st
 int reg_choose(int dir, int B, int H, const DeviceInfo& dev, int fixed_units, int fixed_rows, RecConfig* cfg);
 int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stream);
 
-// Matrix-core forward (16 batch rows x 16 units per workgroup; batch a
-// multiple of 16, hidden size a multiple of 32 up to 256).
-bool mfma_applicable(int dir, int batch, int hidden);
-int mfma_choose(int dir, int batch, int hidden, const DeviceInfo& dev, RecConfig* cfg);
-int mfma_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stream);
-
 }  // namespace rka

@@ -50,8 +50,6 @@ int current_device_info(const DeviceInfo** out) {
 
 namespace {
 
-constexpr int kMaxChunks = 8;
-
 int check_dims(int B, int T, int I, int H) {
     if (B < 1 || T < 1 || H < 1 || I < 1)
         return fail(RKA_ERR_INVALID_ARGUMENT, "batch, seq_len, input_size and hidden_size must be >= 1");
@@ -72,77 +70,23 @@ FwdLayout fwd_layout(int B, int T, int I, int H) {
     return l;
 }
 
-// ------------------------------------------------- backward time chunks ---
-// The backward recurrence can run as `chunks` launches over consecutive time
-// ranges (latest first), with the gradient GEMMs of a finished range (its
-// rows (b, t) of dW_hh, dW_ih and dx) on a second stream while the next
-// range recurs.  Measured on MI355X at B=64, T=512, H=I=256 the overlap
-// loses: GEMM workgroups beside the latency-bound recurrence slow it by
-// 30-60 % and fall behind themselves (step 2.35 ms with 1 chunk, 2.77 with
-// 2, 2.82 with 4, 3.19 with 8), so the automatic choice is one chunk and
-// the chunked path is kept for tuning and tested through the override.
-std::mutex g_chunk_mutex;
-int g_chunk_override = 0;  // 0: automatic
-
-int backward_chunks(int T) {
-    int n;
-    {
-        std::lock_guard<std::mutex> lock(g_chunk_mutex);
-        n = g_chunk_override;
-    }
-    if (n <= 0) n = 1;
-    return std::max(1, std::min(n, T));
-}
-
-// Length of chunk c (0 = the latest steps); earlier chunks take the remainder.
-int chunk_len(int T, int nc, int c) { return T / nc + (c < T % nc ? 1 : 0); }
-
 struct BwdLayout {
-    size_t g, rec, part_hh, part_ih, carry, total;
-    int nc;            // time chunks
-    int ks_hh, ks_ih;  // split-K slices per chunk
+    size_t g, rec, part_hh, part_ih, total;
+    int ks_hh, ks_ih;  // split-K slices
 };
 BwdLayout bwd_layout(int B, int T, int I, int H) {
     BwdLayout l{};
-    l.nc = backward_chunks(T);
-    const int Kc = B * chunk_len(T, l.nc, 0);
-    // resident split-K workgroups per CU; unchunked, the two products share
-    // one launch (gemm_splitk_pair), so each is sized for half the CUs
-    const int wgs = l.nc > 1 ? 0 : 3;
-    const int cus = l.nc > 1 ? 256 : 128;
-    l.ks_hh = choose_ksplit(3 * H, H, Kc, cus, wgs);
-    l.ks_ih = choose_ksplit(3 * H, I, Kc, cus, wgs);
+    const int K = B * T;
+    // the two products share one launch (gemm_splitk_pair), so each is sized
+    // for half the CUs at three resident workgroups per CU
+    l.ks_hh = choose_ksplit(3 * H, H, K, 128, 3);
+    l.ks_ih = choose_ksplit(3 * H, I, K, 128, 3);
     l.g = 0;
     l.rec = align_up((size_t)B * T * 4 * H * sizeof(float), 256);
     l.part_hh = l.rec + align_up(rec_workspace_bytes(B, H), 256);
-    l.part_ih = l.part_hh + align_up(splitk_partial_floats(3 * H, H, l.nc * l.ks_hh) * sizeof(float), 256);
-    l.carry = l.part_ih + align_up(splitk_partial_floats(3 * H, I, l.nc * l.ks_ih) * sizeof(float), 256);
-    l.total = l.carry + (l.nc > 1 ? align_up((size_t)2 * B * H * sizeof(float), 256) : 0);
+    l.part_ih = l.part_hh + align_up(splitk_partial_floats(3 * H, H, l.ks_hh) * sizeof(float), 256);
+    l.total = l.part_ih + align_up(splitk_partial_floats(3 * H, I, l.ks_ih) * sizeof(float), 256);
     return l;
-}
-
-// Per-device second stream (default priority) and events for the chunked
-// backward; enqueueing is serialised per device because the events are
-// shared.
-struct SideStream {
-    std::mutex mutex;
-    hipStream_t stream = nullptr;
-    hipEvent_t ev[kMaxChunks + 1] = {};
-};
-std::mutex g_side_mutex;
-std::vector<SideStream*> g_side;
-
-int side_stream(int dev, SideStream** out) {
-    std::lock_guard<std::mutex> lock(g_side_mutex);
-    if ((int)g_side.size() <= dev) g_side.resize(dev + 1, nullptr);
-    if (!g_side[dev]) {
-        auto* ss = new SideStream();
-        RKA_RETURN_IF_HIP(hipStreamCreateWithFlags(&ss->stream, hipStreamNonBlocking));
-        for (auto& e : ss->ev) RKA_RETURN_IF_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-        g_side[dev] = ss;
-    }
-    *out = g_side[dev];
-    return 0;
 }
 
 // ------------------------------------------------------ stage profiler ---
@@ -191,68 +135,6 @@ class StageScope {
     hipEvent_t start_ = nullptr, stop_ = nullptr;
 };
 
-// Chunked backward (see backward_chunks).  G columns: [0,3H) = (da_n, dr^, dz^)
-// ... laid out as (da_n, dr^, dz^, dn^); G_h = rotation of [0,3H), G_i = [H,4H).
-int backward_chunked(const float* x, const float* h0, const float* w_ih, const float* w_hh, const float* y,
-                     const float* reserve, const float* dy, const float* dhn, float* dx, float* dh0,
-                     float* dw_ih, float* dw_hh, float* db_ih, float* db_hh, char* ws, const BwdLayout& l,
-                     int B, int T, int I, int H, hipStream_t s) {
-    const DeviceInfo* dev = nullptr;
-    RKA_RETURN_IF_ERR(current_device_info(&dev));
-    if (l.nc > kMaxChunks) return fail(RKA_ERR_INVALID_ARGUMENT, "backward: too many time chunks");
-    SideStream* ss = nullptr;
-    RKA_RETURN_IF_ERR(side_stream(dev->device, &ss));
-    std::lock_guard<std::mutex> lock(ss->mutex);
-    hipStream_t side = ss->stream;
-    float* g = reinterpret_cast<float*>(ws + l.g);
-    float* part_hh = reinterpret_cast<float*>(ws + l.part_hh);
-    float* part_ih = reinterpret_cast<float*>(ws + l.part_ih);
-    float* carry[2] = {reinterpret_cast<float*>(ws + l.carry), reinterpret_cast<float*>(ws + l.carry) + (size_t)B * H};
-    int t_hi = T;
-    for (int c = 0; c < l.nc; ++c) {
-        const int L = chunk_len(T, l.nc, c);
-        const int t_lo = t_hi - L;
-        const float* dh_in = c == 0 ? dhn : carry[(c - 1) & 1];
-        float* dh_out = c == l.nc - 1 ? dh0 : carry[c & 1];
-        {
-            StageScope scope(2, s);
-            RKA_RETURN_IF_ERR(launch_rec_backward_range(dy, dh_in, reserve, h0, y, w_hh, g, dh_out, ws + l.rec,
-                                                        l.part_hh - l.rec, B, T, H, t_lo, t_hi, c == 0, s));
-        }
-        RKA_RETURN_IF_HIP(hipEventRecord(ss->ev[c], s));
-        RKA_RETURN_IF_HIP(hipStreamWaitEvent(side, ss->ev[c], 0));
-        // rows (b, t_lo .. t_hi-1) of every sequence
-        const SegMap seg{L, T, t_lo};
-        const int Kc = B * L;
-        GemmOperand gh{g, 4 * H, 1, 0, nullptr, seg};
-        GemmOperand hprev{y, H, 1, T, h0, seg};
-        GemmOperand gi{g + H, 4 * H, 1, 0, nullptr, seg};
-        GemmOperand xk{x, I, 1, 0, nullptr, seg};
-        {
-            StageScope scope(3, side);
-            RKA_RETURN_IF_ERR(gemm_splitk_partials(3 * H, H, Kc, gh, hprev, true, part_hh, l.ks_hh, c * l.ks_hh,
-                                                   l.nc * l.ks_hh, side));
-            RKA_RETURN_IF_ERR(gemm_splitk_partials(3 * H, I, Kc, gi, xk, true, part_ih, l.ks_ih, c * l.ks_ih,
-                                                   l.nc * l.ks_ih, side));
-        }
-        if (dx) {
-            GemmOperand ga{g + H, 4 * H, 0, 0, nullptr, seg};
-            GemmOperand wk{w_ih, I, 1, 0, nullptr};
-            StageScope scope(5, side);
-            RKA_RETURN_IF_ERR(gemm_direct(Kc, I, 3 * H, ga, wk, nullptr, dx, I, side, seg));
-        }
-        t_hi = t_lo;
-    }
-    {
-        StageScope scope(4, side);
-        RKA_RETURN_IF_ERR(splitk_reduce(3 * H, H, part_hh, l.nc * l.ks_hh, H, dw_hh, H, db_hh, side));
-        RKA_RETURN_IF_ERR(splitk_reduce(3 * H, I, part_ih, l.nc * l.ks_ih, 0, dw_ih, I, db_ih, side));
-    }
-    RKA_RETURN_IF_HIP(hipEventRecord(ss->ev[l.nc], side));
-    RKA_RETURN_IF_HIP(hipStreamWaitEvent(s, ss->ev[l.nc], 0));
-    return 0;
-}
-
 }  // namespace
 }  // namespace rka
 
@@ -260,7 +142,7 @@ using namespace rka;
 
 extern "C" {
 
-int rka_version(void) { return 1; }
+int rka_version(void) { return 2; }
 
 const char* rka_last_error(void) { return t_last_error.c_str(); }
 
@@ -346,9 +228,6 @@ int rka_gru_backward(const float* x, const float* h0, const float* w_ih, const f
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     char* ws = reinterpret_cast<char*>(workspace);
     float* g = reinterpret_cast<float*>(ws + l.g);
-    if (l.nc > 1)
-        return backward_chunked(x, h0, w_ih, w_hh, y, reserve, dy, dhn, dx, dh0, dw_ih, dw_hh, db_ih, db_hh, ws, l,
-                                B, T, I, H, s);
     {
         StageScope scope(2, s);
         RKA_RETURN_IF_ERR(launch_rec_backward(dy, dhn, reserve, h0, y, w_hh, g, dh0, ws + l.rec,
@@ -438,22 +317,10 @@ int rka_set_recurrence_config(int dir, int kind, int units, int param) {
     } else if (kind == REC_REGISTER) {
         if (!ok_p || !(units == 0 || units == 64))
             return fail(RKA_ERR_INVALID_ARGUMENT, "register: units 64 (or 0), rows 1, 2 or 4 (0 = auto)");
-    } else if (kind == REC_MFMA) {
-        if (dir != 0 || units != 0 || param != 0)
-            return fail(RKA_ERR_INVALID_ARGUMENT, "mfma: forward only (dir 0), units and param 0");
     } else {
-        return fail(RKA_ERR_INVALID_ARGUMENT, "kind must be 0 (auto), 1 (tiled), 2 (register) or 3 (mfma)");
+        return fail(RKA_ERR_INVALID_ARGUMENT, "kind must be 0 (auto), 1 (tiled) or 2 (register)");
     }
     set_rec_override(dir, kind, units, param);
-    return 0;
-}
-
-int rka_set_backward_chunks(int chunks) {
-    clear_error();
-    if (chunks < 0 || chunks > kMaxChunks)
-        return fail(RKA_ERR_INVALID_ARGUMENT, "chunks must be 0 (automatic) .. " + std::to_string(kMaxChunks));
-    std::lock_guard<std::mutex> lock(g_chunk_mutex);
-    g_chunk_override = chunks;
     return 0;
 }
 
@@ -491,18 +358,10 @@ int rka_recurrence_abort_count(unsigned long long* count) {
     return rec_abort_count(count);
 }
 
-int rka_backward_chunks(int seq_len) {
+int rka_describe_recurrence(int dir, int batch, int hidden_size, int* out, int n_out) {
     clear_error();
-    if (seq_len < 1) {
-        set_error("seq_len must be >= 1");
-        return -1;
-    }
-    return backward_chunks(seq_len);
-}
-
-int rka_describe_recurrence(int dir, int batch, int hidden_size, int out10[10]) {
-    clear_error();
-    if ((dir != 0 && dir != 1) || !out10) return fail(RKA_ERR_INVALID_ARGUMENT, "dir must be 0 or 1");
+    if ((dir != 0 && dir != 1) || !out || n_out < 1)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "dir must be 0 or 1, out non-NULL and n_out >= 1");
     RKA_RETURN_IF_ERR(check_dims(batch, 1, 1, hidden_size));
     const DeviceInfo* dev = nullptr;
     RKA_RETURN_IF_ERR(current_device_info(&dev));
@@ -510,7 +369,7 @@ int rka_describe_recurrence(int dir, int batch, int hidden_size, int out10[10]) 
     RKA_RETURN_IF_ERR(choose_rec_config(dir, batch, hidden_size, *dev, &c));
     const int v[10] = {c.kind,      c.groups, c.slices,    c.units,    c.rows,
                        c.pair_waves, c.chunk, c.lds_bytes, c.launches, c.batch_per_launch};
-    for (int i = 0; i < 10; ++i) out10[i] = v[i];
+    for (int i = 0; i < 10 && i < n_out; ++i) out[i] = v[i];
     return 0;
 }
 

@@ -122,7 +122,7 @@ int set_gemm_tiles(int mode);
 int choose_ksplit(int m, int n, int k, int num_cus, int wgs_per_cu);
 
 // ----------------------------------------------------------- recurrence ---
-enum RecKind { REC_AUTO = 0, REC_TILED = 1, REC_REGISTER = 2, REC_MFMA = 3 };
+enum RecKind { REC_AUTO = 0, REC_TILED = 1, REC_REGISTER = 2 };
 
 // A recurrence runs as `launches` kernel launches over consecutive batch
 // slices of `batch_per_launch` rows (the last one possibly shorter), each a

@@ -289,32 +289,11 @@ def rec_kind(request, hip_lib):
         _lib.set_recurrence_config(d, 0, 0, 0)
 
 
-@pytest.fixture
-def mfma_forward(hip_lib):
-    """Forces the matrix-core forward (kind 3; the backward stays automatic)
-    for one test, then restores the automatic choice."""
-    from rnn_kernel_amd import _lib
-
-    _lib.set_recurrence_config(0, 3, 0, 0)
-    yield "mfma"
-    _lib.set_recurrence_config(0, 0, 0, 0)
-
-
-# shapes the matrix-core forward takes, one per K width (H / 32 = 1 .. 8),
-# with T = 1 and a c4-sized batch
-MFMA_SHAPES = [(16, 5, 8, 32), (32, 7, 16, 64), (48, 4, 8, 96), (16, 6, 4, 128), (64, 9, 16, 160),
-               (32, 3, 8, 192), (16, 4, 8, 224), (256, 6, 16, 256), (64, 1, 1, 256)]
-
-
 @pytest.mark.parametrize("B,T,I,H", LAYER_SHAPES + [(3, 4, 8, 320), (2, 3, 5, 512), (64, 3, 16, 768), (200, 2, 8, 768),
-                                     (256, 2, 8, 512), (83, 4, 8, 130)] + MFMA_SHAPES)
+                                     (256, 2, 8, 512), (83, 4, 8, 130), (256, 6, 16, 256), (64, 1, 1, 256),
+                                     (48, 4, 8, 96), (16, 4, 8, 224)])
 def test_layer_forward_backward_matches_oracle(gpu, oracle, rec_kind, B, T, I, H):
     _check_layer_against_oracle(gpu, oracle, rec_kind, B, T, I, H)
-
-
-@pytest.mark.parametrize("B,T,I,H", MFMA_SHAPES)
-def test_layer_with_matrix_core_forward_matches_oracle(gpu, oracle, mfma_forward, B, T, I, H):
-    _check_layer_against_oracle(gpu, oracle, mfma_forward, B, T, I, H)
 
 
 @pytest.fixture
@@ -390,77 +369,6 @@ def _check_layer_against_oracle(gpu, oracle, rec_kind, B, T, I, H):
     assert _rel(pd["bias_hh"].grad, ref.db_hh) <= GRAD_REL
 
 
-@pytest.fixture
-def backward_chunks(hip_lib):
-    """Sets the backward's time-chunk count for one test, then restores auto."""
-    from rnn_kernel_amd import _lib
-
-    def set_chunks(n):
-        _lib.set_backward_chunks(n)
-
-    yield set_chunks
-    _lib.set_backward_chunks(0)
-
-
-@pytest.mark.parametrize("B,T,I,H,chunks", [
-    (3, 7, 5, 33, 2),      # odd lengths: chunks of 4 and 3 steps
-    (3, 7, 5, 33, 7),      # one step per chunk
-    (2, 9, 4, 130, 4),     # odd hidden size, tails
-    (5, 16, 8, 64, 8),     # the maximum chunk count
-    (4, 5, 3, 256, 3),     # register kernel at H = 256
-    (2, 3, 2, 40, 8),      # more chunks asked than steps: clamped to T
-    (8, 9, 4, 256, 3),     # H = 256 with groups on one XCD (plain publishing stores) across ranges
-    (3, 8, 4, 200, 3),     # four slices, the last one partial, across ranges
-    (16, 9, 4, 256, 3),    # a whole 16-row group
-])
-def test_chunked_backward_matches_oracle(gpu, oracle, rec_kind, backward_chunks, B, T, I, H, chunks):
-    """The backward in time chunks (recurrence per range, gradient GEMMs of a
-    finished range on a second stream) against the oracle."""
-    from rnn_kernel_amd import GRUFunction, _lib
-
-    backward_chunks(chunks)
-    print(f"chunked backward B={B} T={T} I={I} H={H} chunks={_lib.backward_chunks(T)} kind={rec_kind}", flush=True)
-    assert _lib.backward_chunks(T) == min(chunks, T)
-    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=31 * B + 7 * T + H + chunks)
-    f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
-                       p["bias_ih"].numpy(), p["bias_hh"].numpy())
-    ref = oracle.backward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(), f.y, f.cache,
-                          dy.numpy(), dhn.numpy())
-    xd = x.to(gpu).requires_grad_(True)
-    h0d = h0.to(gpu).requires_grad_(True)
-    pd = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
-    y, hn = GRUFunction.apply(xd, h0d, pd["weight_ih"], pd["weight_hh"], pd["bias_ih"], pd["bias_hh"])
-    torch.autograd.backward([y, hn], [dy.to(gpu), dhn.to(gpu)[None]])
-    torch.cuda.synchronize()
-    assert _rel(xd.grad, ref.dx) <= GRAD_REL
-    assert _rel(h0d.grad, ref.dh0) <= GRAD_REL
-    assert _rel(pd["weight_ih"].grad, ref.dw_ih) <= GRAD_REL
-    assert _rel(pd["weight_hh"].grad, ref.dw_hh) <= GRAD_REL
-    assert _rel(pd["bias_ih"].grad, ref.db_ih) <= GRAD_REL
-    assert _rel(pd["bias_hh"].grad, ref.db_hh) <= GRAD_REL
-
-
-def test_chunked_backward_without_input_gradient(gpu, oracle, backward_chunks):
-    """x without requires_grad: dx is skipped in every chunk, the weight
-    gradients are unchanged."""
-    from rnn_kernel_amd import GRUFunction
-
-    backward_chunks(3)
-    B, T, I, H = 4, 10, 6, 48
-    p, x, h0, dy, dhn = _layer_inputs(B, T, I, H, seed=5)
-    f = oracle.forward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(),
-                       p["bias_ih"].numpy(), p["bias_hh"].numpy())
-    ref = oracle.backward(x.numpy(), h0.numpy(), p["weight_ih"].numpy(), p["weight_hh"].numpy(), f.y, f.cache,
-                          dy.numpy(), None)
-    pd = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
-    y, _ = GRUFunction.apply(x.to(gpu), h0.to(gpu), pd["weight_ih"], pd["weight_hh"], pd["bias_ih"], pd["bias_hh"])
-    y.backward(dy.to(gpu))
-    torch.cuda.synchronize()
-    assert _rel(pd["weight_ih"].grad, ref.dw_ih) <= GRAD_REL
-    assert _rel(pd["weight_hh"].grad, ref.dw_hh) <= GRAD_REL
-    assert _rel(pd["bias_hh"].grad, ref.db_hh) <= GRAD_REL
-
-
 def test_recurrence_reserve_layout_matches_oracle_cache(gpu, oracle, hip_lib):
     """The forward recurrence's reserve is (r, z, n, a_n) per [b, t, unit]."""
     from rnn_kernel_amd import _lib
@@ -508,12 +416,6 @@ def test_timed_out_waits_abort_with_nan_in_every_unwritten_output(gpu, oracle, h
     (rka_recurrence_abort_count) must grow by one per call, which
     check_recurrences() turns into RecurrenceAbortedError."""
     _check_abort_path(gpu, oracle, hip_lib, rec_kind, B, T, H)
-
-
-@pytest.mark.parametrize("B,T,H", [(16, 32, 256), (64, 24, 256)])
-def test_timed_out_waits_abort_matrix_core_forward(gpu, oracle, hip_lib, mfma_forward, B, T, H):
-    """The forced-abort test with the matrix-core forward."""
-    _check_abort_path(gpu, oracle, hip_lib, mfma_forward, B, T, H)
 
 
 def _check_abort_path(gpu, oracle, hip_lib, rec_kind, B, T, H):
@@ -854,24 +756,6 @@ def test_recurrences_progress_beside_a_concurrent_kernel(gpu, B, H):
         for a, b in zip(solo, busy):
             assert torch.isfinite(b).all()
             assert torch.equal(a, b)
-
-
-def test_matrix_core_forward_is_forced_only(gpu, hip_lib):
-    """The automatic choice keeps the register-resident forward (four rows per
-    workgroup at B = 256); forcing kind 3 describes the matrix-core
-    decomposition: 16 groups of 16 rows x 16 slices of 16 units, one launch."""
-    from rnn_kernel_amd import _lib
-
-    assert _lib.describe_recurrence(0, 256, 256)["kind"] == "register"
-    _lib.set_recurrence_config(0, 3, 0, 0)
-    try:
-        d = _lib.describe_recurrence(0, 256, 256)
-        print("forced matrix-core forward at B=256 H=256:", d, flush=True)
-        assert d["kind"] == "mfma" and d["launches"] == 1 and (d["groups"], d["slices"]) == (16, 16)
-        with pytest.raises(_lib.RKAError):
-            _lib.describe_recurrence(0, 300, 256)  # not whole 16-row groups
-    finally:
-        _lib.set_recurrence_config(0, 0, 0, 0)
 
 
 @pytest.mark.parametrize("H,fwd_rows,bwd_rows", [(200, 2, 4), (256, 2, 2), (160, 4, 4), (64, 4, 2)])

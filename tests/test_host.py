@@ -2,6 +2,7 @@
 symbol include/rnn_kernel_amd.h declares, module construction / validation
 behaves like the reference's (error types and messages), and the drop-in
 shims for the reference's import paths resolve."""
+import ctypes
 import json
 import os
 import re
@@ -45,7 +46,7 @@ def test_library_size_queries_without_gpu(hip_lib):
     bwd = hip_lib.rka_gru_backward_workspace_bytes(B, T, I, H)
     assert bwd >= B * T * 4 * H * 4
     assert hip_lib.rka_gru_forward_workspace_bytes(0, T, I, H) == 0
-    assert hip_lib.rka_version() == 1
+    assert hip_lib.rka_version() == 2
 
 
 def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
@@ -60,19 +61,18 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     assert hip_lib.rka_set_recurrence_config(0, 5, 0, 0) == 1001   # bad kind
     assert hip_lib.rka_set_recurrence_config(0, 1, 3, 0) == 1001   # units must divide 64
     assert hip_lib.rka_set_recurrence_config(1, 2, 0, 3) == 1001   # rows 1, 2 or 4
-    assert hip_lib.rka_set_recurrence_config(1, 3, 0, 0) == 1001   # the matrix-core kernel is forward only
-    assert hip_lib.rka_set_recurrence_config(0, 3, 16, 0) == 1001  # and takes no units / rows
+    assert hip_lib.rka_set_recurrence_config(0, 3, 0, 0) == 1001   # bad kind
     assert hip_lib.rka_set_recurrence_config(0, 4, 0, 0) == 1001   # bad kind
     assert hip_lib.rka_set_recurrence_config(0, 0, 0, 0) == 0
-    assert hip_lib.rka_set_backward_chunks(-1) == 1001
-    assert hip_lib.rka_set_backward_chunks(9) == 1001
     assert hip_lib.rka_set_spin_limit(-1) == 1001
     assert hip_lib.rka_set_spin_limit((1 << 30) + 1) == 1001   # above the largest poll bound
     assert hip_lib.rka_recurrence_abort_count(None) == 1001
     assert hip_lib.rka_set_stall_block(-2) == 1001
     assert hip_lib.rka_set_stall_block(-1) == 0
     assert hip_lib.rka_set_spin_limit(0) == 0
-    assert hip_lib.rka_backward_chunks(0) == -1
+    out = (ctypes.c_int * 2)()
+    assert hip_lib.rka_describe_recurrence(0, 4, 16, out, 0) == 1001  # n_out must be >= 1
+    assert hip_lib.rka_describe_recurrence(2, 4, 16, out, 2) == 1001  # bad direction
     assert hip_lib.rka_set_gemm_tiles(2) == 1001
     assert hip_lib.rka_set_gemm_tiles(-1) == 1001
     assert hip_lib.rka_set_gemm_tiles(1) == 0 and hip_lib.rka_set_gemm_tiles(0) == 0
@@ -81,24 +81,13 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     assert hip_lib.rka_set_exchange_stores(1) == 0 and hip_lib.rka_set_exchange_stores(0) == 0
 
 
-def test_backward_chunk_policy_without_gpu(hip_lib):
-    """Automatic: one time chunk; an override is clamped to seq_len; the
-    chunked layout holds the G buffer, the exchange words, per-chunk split-K
-    partials and the two dh carry buffers."""
-    from rnn_kernel_amd import _lib
-
+def test_backward_workspace_holds_gate_gradients_exchange_and_partials(hip_lib):
+    """The backward workspace holds the G buffer [B,T,4H], the recurrence's
+    exchange state and the split-K partials of both weight-gradient products."""
     B, T, I, H = 64, 100, 256, 256
-    try:
-        assert _lib.backward_chunks(512) == 1 and _lib.backward_chunks(127) == 1
-        one = hip_lib.rka_gru_backward_workspace_bytes(B, T, I, H)
-        _lib.set_backward_chunks(3)
-        assert _lib.backward_chunks(2) == 2 and _lib.backward_chunks(512) == 3
-        chunked = hip_lib.rka_gru_backward_workspace_bytes(B, T, I, H)
-        g_bytes, carry_bytes = B * T * 4 * H * 4, 2 * B * H * 4
-        assert chunked != one
-        assert chunked > g_bytes + hip_lib.rka_gru_recurrence_workspace_bytes(B, H) + carry_bytes
-    finally:
-        _lib.set_backward_chunks(0)
+    need = hip_lib.rka_gru_backward_workspace_bytes(B, T, I, H)
+    g_bytes = B * T * 4 * H * 4
+    assert need > g_bytes + hip_lib.rka_gru_recurrence_workspace_bytes(B, H) + 2 * 3 * H * H * 4
 
 
 def test_module_construction_and_validation_messages():

@@ -29,14 +29,26 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+# calls in a row on the shared static state, each later one smaller:
+#   c2-like one-row launch, then a small odd shape;
+#   at the static limit (B H = 262144): B = 1024 at H = 256 runs the register
+#   kernel as several batch-slice launches (the last slice's words end at the
+#   array's end), H = 512 the LDS-tiled kernel; then the small odd shape
+SEQUENCES = [
+    ((64, 40, 256, 1), (5, 7, 130, 2)),
+    ((1024, 6, 256, 3), (512, 5, 512, 4), (5, 7, 130, 5)),
+]
+
+
 @pytest.mark.parametrize("with_reserve", [True, False])
-def test_noalloc_forward_matches_workspace_forward(gpu, hip_lib, with_reserve):
+@pytest.mark.parametrize("sequence", SEQUENCES)
+def test_noalloc_forward_matches_workspace_forward(gpu, hip_lib, with_reserve, sequence):
     from rnn_kernel_amd import _lib
 
     stream = torch.cuda.current_stream().cuda_stream
-    # two calls in a row on the shared static state, the second smaller
-    for B, T, H, seed in ((64, 40, 256, 1), (5, 7, 130, 2)):
-        print(f"noalloc forward B={B} T={T} H={H} reserve={with_reserve}", flush=True)
+    for B, T, H, seed in sequence:
+        print(f"noalloc forward B={B} T={T} H={H} reserve={with_reserve} fwd={_lib.describe_recurrence(0, B, H)}",
+              flush=True)
         gx, whh, bhh, h0 = _inputs(B, T, H, seed, gpu)
         y_ref, hn_ref, res_ref = _outputs(B, T, H, gpu, with_reserve)
         ws_bytes = hip_lib.rka_gru_recurrence_workspace_bytes(B, H)
