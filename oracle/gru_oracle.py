@@ -217,6 +217,56 @@ def stack_forward_backward(x, hx, params: Sequence[dict], dy, dhn=None, dtype=np
     return StackResult(fwds[-1].y, np.stack(hns, 0), g_out, dhx, grads)
 
 
+def stack_rows_parallel(x, hx, params: Sequence[dict], dy_of, threads: int, dhn=None,
+                        dtype=np.float64) -> StackResult:
+    """``stack_forward_backward`` with the batch rows split over ``threads``
+    threads.  ``dy_of(y, a, b)`` gives the gradient of the last layer's
+    output for rows ``a:b`` from their output ``y`` (e.g. the MSE gradient
+    against the target's rows), so that the gradient can depend on the
+    forward's result.  Rows are independent sequences: y, h_n, dx and d hx
+    are each row's own results, and every weight and bias gradient is the
+    chunks' sums added in chunk order."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    x = np.asarray(x)
+    B = x.shape[0]
+    L = len(params)
+    chunks = _row_chunks(B, threads)
+
+    def run(c):
+        a, b = c
+        hxc = None if hx is None else np.asarray(hx)[:, a:b]
+        # forward of the stack for these rows, then the output gradient
+        layer_in, fwds = [np.asarray(x[a:b], dtype=dtype)], []
+        Hh = np.asarray(params[0]["weight_hh"]).shape[1]
+        h0s = np.zeros((L, b - a, Hh), dtype=dtype) if hxc is None else np.asarray(hxc, dtype=dtype)
+        for l in range(L):
+            p = params[l]
+            f = forward(layer_in[-1], h0s[l], p["weight_ih"], p["weight_hh"], p["bias_ih"], p["bias_hh"], dtype=dtype)
+            fwds.append(f)
+            layer_in.append(f.y)
+        g_out = np.asarray(dy_of(fwds[-1].y, a, b), dtype=dtype)
+        grads, dhx = [None] * L, np.zeros((L, b - a, Hh), dtype=dtype)
+        for l in reversed(range(L)):
+            p = params[l]
+            bw = backward(layer_in[l], h0s[l], p["weight_ih"], p["weight_hh"], fwds[l].y, fwds[l].cache, g_out,
+                          None if dhn is None else np.asarray(dhn)[l, a:b], dtype=dtype, need_dx=True)
+            grads[l] = {"weight_ih": bw.dw_ih, "weight_hh": bw.dw_hh, "bias_ih": bw.db_ih, "bias_hh": bw.db_hh}
+            dhx[l] = bw.dh0
+            g_out = bw.dx
+        return fwds[-1].y, np.stack([f.hn for f in fwds], 0), g_out, dhx, grads
+
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        parts = list(ex.map(run, chunks))
+    grads = [{k: v.copy() for k, v in parts[0][4][l].items()} for l in range(L)]
+    for part in parts[1:]:
+        for l in range(L):
+            for k in grads[l]:
+                grads[l][k] += part[4][l][k]
+    return StackResult(np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts], axis=1),
+                       np.concatenate([p[2] for p in parts]), np.concatenate([p[3] for p in parts], axis=1), grads)
+
+
 # ------------------------------------------------ harness-side operations ---
 # float64 restatements of the benchmark harness's head, loss and optimiser
 # (train_ops_oracle.c; reference rnn_benchmark.py:510,525,636,722).

@@ -6,10 +6,14 @@
  * library built from it.  The product path (rnn_kernel_amd) never calls it.
  *
  * It is compiled twice by gru_oracle.c, once with REAL=double and once with
- * REAL=float, giving the *_f64 and *_f32 entry points.  Loops are plain
- * scalar C in the order the equations are written; there is no blocking or
- * threading, so the fp32 variant's summation order is the naive left-to-right
- * one and the fp64 variant bounds its rounding error.
+ * REAL=float, giving the *_f64 and *_f32 entry points.  Every sum is taken
+ * left to right in increasing index order (there is no blocking, splitting or
+ * threading of a sum), so the fp32 variant's summation order is the naive one
+ * and the fp64 variant bounds its rounding error.  The loops over a sum's
+ * index are arranged so that inner loops run over contiguous memory (a
+ * transposed copy of the weights in the forward, arrays of running sums in
+ * the backward); that reorders independent sums against one another, never
+ * the terms of one sum.
  *
  * Equations follow the reference:
  *   input projection  Gx = x W_ih^T + b_ih
@@ -65,26 +69,38 @@ int ORC_FN(oracle_gru_forward)(int B, int T, int I, int H,
     REAL* gx = (REAL*)malloc(sizeof(REAL) * (size_t)G3);
     REAL* ah = (REAL*)malloc(sizeof(REAL) * (size_t)G3);
     REAL* hprev = (REAL*)malloc(sizeof(REAL) * (size_t)H);
-    if (!gx || !ah || !hprev) {
-        free(gx); free(ah); free(hprev);
+    /* W_ih^T [I][3H] and W_hh^T [H][3H]: row k holds the k-th term's weights
+     * of every gate row j, so the running sums of all j advance together */
+    REAL* wiT = (REAL*)malloc(sizeof(REAL) * (size_t)I * G3);
+    REAL* whT = (REAL*)malloc(sizeof(REAL) * (size_t)H * G3);
+    if (!gx || !ah || !hprev || !wiT || !whT) {
+        free(gx); free(ah); free(hprev); free(wiT); free(whT);
         return 1;
+    }
+    for (int j = 0; j < G3; ++j) {
+        for (int k = 0; k < I; ++k) wiT[(size_t)k * G3 + j] = w_ih[(size_t)j * I + k];
+        for (int k = 0; k < H; ++k) whT[(size_t)k * G3 + j] = w_hh[(size_t)j * H + k];
     }
     for (int b = 0; b < B; ++b) {
         for (int k = 0; k < H; ++k) hprev[k] = h0[(size_t)b * H + k];
         for (int t = 0; t < T; ++t) {
             const REAL* xt = x + ((size_t)b * T + t) * I;
-            for (int j = 0; j < G3; ++j) {
-                REAL acc = 0;
-                const REAL* w = w_ih + (size_t)j * I;
-                for (int k = 0; k < I; ++k) acc += w[k] * xt[k];
-                gx[j] = acc + b_ih[j];
+            /* gx[j] = (sum_k W_ih[j][k] x_t[k], k = 0, 1, ...) + b_ih[j] */
+            for (int j = 0; j < G3; ++j) gx[j] = 0;
+            for (int k = 0; k < I; ++k) {
+                const REAL* w = wiT + (size_t)k * G3;
+                const REAL xk = xt[k];
+                for (int j = 0; j < G3; ++j) gx[j] += w[j] * xk;
             }
-            for (int j = 0; j < G3; ++j) {
-                REAL acc = 0;
-                const REAL* w = w_hh + (size_t)j * H;
-                for (int k = 0; k < H; ++k) acc += w[k] * hprev[k];
-                ah[j] = acc + b_hh[j];
+            for (int j = 0; j < G3; ++j) gx[j] += b_ih[j];
+            /* ah[j] = (sum_k W_hh[j][k] h_{t-1}[k]) + b_hh[j] */
+            for (int j = 0; j < G3; ++j) ah[j] = 0;
+            for (int k = 0; k < H; ++k) {
+                const REAL* w = whT + (size_t)k * G3;
+                const REAL hk = hprev[k];
+                for (int j = 0; j < G3; ++j) ah[j] += w[j] * hk;
             }
+            for (int j = 0; j < G3; ++j) ah[j] += b_hh[j];
             REAL* yt = y + ((size_t)b * T + t) * H;
             REAL* ct = cache ? cache + ((size_t)b * T + t) * 4 * H : NULL;
             for (int u = 0; u < H; ++u) {
@@ -105,7 +121,7 @@ int ORC_FN(oracle_gru_forward)(int B, int T, int I, int H,
             for (int u = 0; u < H; ++u) hn[(size_t)b * H + u] = hprev[u];
         }
     }
-    free(gx); free(ah); free(hprev);
+    free(gx); free(ah); free(hprev); free(wiT); free(whT);
     return 0;
 }
 
@@ -128,8 +144,10 @@ int ORC_FN(oracle_gru_backward)(int B, int T, int I, int H,
     REAL* gi = (REAL*)malloc(sizeof(REAL) * (size_t)G3);
     REAL* gh = (REAL*)malloc(sizeof(REAL) * (size_t)G3);
     REAL* dhp = (REAL*)malloc(sizeof(REAL) * (size_t)H);
-    if (!dh || !gi || !gh || !dhp) {
-        free(dh); free(gi); free(gh); free(dhp);
+    REAL* sh = (REAL*)malloc(sizeof(REAL) * (size_t)H);  /* running sums of G_h W_hh */
+    REAL* sx = (REAL*)malloc(sizeof(REAL) * (size_t)I);  /* running sums of G_i W_ih */
+    if (!dh || !gi || !gh || !dhp || !sh || !sx) {
+        free(dh); free(gi); free(gh); free(dhp); free(sh); free(sx);
         return 1;
     }
     memset(dw_ih, 0, sizeof(REAL) * (size_t)G3 * I);
@@ -157,12 +175,14 @@ int ORC_FN(oracle_gru_backward)(int B, int T, int I, int H,
                 gh[u] = drh;     gh[H + u] = dzh;     gh[2 * H + u] = dan;
                 dhp[u] = g * z;
             }
-            /* dh_{t-1} = g z + G_h W_hh */
-            for (int k = 0; k < H; ++k) {
-                REAL acc = 0;
-                for (int j = 0; j < G3; ++j) acc += gh[j] * w_hh[(size_t)j * H + k];
-                dh[k] = dhp[k] + acc;
+            /* dh_{t-1}[k] = g z + (sum_j G_h[j] W_hh[j][k], j = 0, 1, ...) */
+            for (int k = 0; k < H; ++k) sh[k] = 0;
+            for (int j = 0; j < G3; ++j) {
+                const REAL* w = w_hh + (size_t)j * H;
+                const REAL gj = gh[j];
+                for (int k = 0; k < H; ++k) sh[k] += gj * w[k];
             }
+            for (int k = 0; k < H; ++k) dh[k] = dhp[k] + sh[k];
             /* parameter gradients */
             const REAL* xt = x + ((size_t)b * T + t) * I;
             for (int j = 0; j < G3; ++j) {
@@ -174,17 +194,20 @@ int ORC_FN(oracle_gru_backward)(int B, int T, int I, int H,
                 db_hh[j] += gh[j];
             }
             if (dx) {
+                /* dx_t[k] = sum_j G_i[j] W_ih[j][k], j = 0, 1, ... */
                 REAL* dxt = dx + ((size_t)b * T + t) * I;
-                for (int k = 0; k < I; ++k) {
-                    REAL acc = 0;
-                    for (int j = 0; j < G3; ++j) acc += gi[j] * w_ih[(size_t)j * I + k];
-                    dxt[k] = acc;
+                for (int k = 0; k < I; ++k) sx[k] = 0;
+                for (int j = 0; j < G3; ++j) {
+                    const REAL* w = w_ih + (size_t)j * I;
+                    const REAL gj = gi[j];
+                    for (int k = 0; k < I; ++k) sx[k] += gj * w[k];
                 }
+                for (int k = 0; k < I; ++k) dxt[k] = sx[k];
             }
         }
         for (int u = 0; u < H; ++u) dh0[(size_t)b * H + u] = dh[u];
     }
-    free(dh); free(gi); free(gh); free(dhp);
+    free(dh); free(gi); free(gh); free(dhp); free(sh); free(sx);
     return 0;
 }
 

@@ -906,21 +906,83 @@ def test_config3_hidden_sweep_matches_torch_gru(gpu, H):
     _assert_parity(res, f"c3 H={H}")
 
 
-def test_config4_stacked_two_layers_matches_torch_gru(gpu):
+def _oracle_errors(ours, ref, L):
+    """Max-abs errors of out / h_n and relative errors of every gradient of a
+    full-size run against the float64 oracle (stack_rows_parallel result)."""
+    errs = {"out": _maxabs(ours["out"], ref.y), "hn": _maxabs(ours["hn"], ref.hn), "dx": _rel(ours["dx"], ref.dx),
+            "dh0": _rel(ours["dh0"], ref.dhx)}
+    for l in range(L):
+        for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh"):
+            errs[f"{n}_l{l}"] = _rel(ours[f"{n}_l{l}"], ref.grads[l][n])
+    return errs
+
+
+def _assert_oracle_errors(errs, label):
+    print(f"  {label} vs the float64 oracle:", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert errs["out"] <= OUT_ATOL and errs["hn"] <= OUT_ATOL, label
+    for k, v in errs.items():
+        if k not in ("out", "hn"):
+            assert v <= GRAD_REL, (label, k, v)
+
+
+def _oracle_params(torch_gru, L):
+    return [{n: getattr(torch_gru, f"{n}_l{l}").detach().cpu().double().numpy()
+             for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")} for l in range(L)]
+
+
+def test_config4_stacked_two_layers_matches_torch_gru_and_the_oracle(gpu, oracle):
+    """L=2, I=H=256, B=256, T=1024, MSE loss: every output and gradient of both
+    layers against torch.nn.GRU fp32 on the GPU and against the float64
+    oracle's two-layer stack at full size (layer composition of
+    src/rnn_kernel/a100/prod/gru.py:699-728; batch rows split over up to 16
+    host threads, each chunk's output gradient the MSE gradient of its own
+    forward result)."""
+    import os
+
     print("config4 L=2 B=256 T=1024 H=256", flush=True)
-    res, _ = _torch_reference(gpu, 2, 256, 256, 256, 1024, seed=44, h0_scale=0.0)
+    res, (torch_gru, x, h0, target) = _torch_reference(gpu, 2, 256, 256, 256, 1024, seed=44, h0_scale=0.0)
     _assert_parity(res, "c4")
+    tgt = target.double().numpy()
+    scale = 2.0 / tgt.size
+    ref = oracle.stack_rows_parallel(x.double().numpy(), h0.double().numpy(), _oracle_params(torch_gru, 2),
+                                     lambda y, a, b: scale * (y - tgt[a:b]), threads=min(16, os.cpu_count() or 1))
+    _assert_oracle_errors(_oracle_errors(res["ours"], ref, 2), "c4")
 
 
-def test_config5_chunked_bptt_matches_full_sequence(gpu):
-    """I=128, H=256, B=16, T=4096 as 8 chunks of 512 carrying h (no detach),
-    h0 ~ 0.5 N(0,1), 5% of [B,T] rows of x scaled x10."""
-    print("config5 chunked", flush=True)
-
+def _config5_inputs():
     def saturate(x):
         g = torch.Generator().manual_seed(4242)
         mask = torch.rand(x.shape[0], x.shape[1], generator=g) < 0.05
         return torch.where(mask[..., None], x * 10.0, x)
 
-    res, _ = _torch_reference(gpu, 1, 128, 256, 16, 4096, seed=45, h0_scale=0.5, x_hook=saturate, chunks=8)
+    return dict(L=1, I=128, H=256, B=16, T=4096, seed=45, h0_scale=0.5, x_hook=saturate)
+
+
+def test_config5_chunked_bptt_matches_torch_gru_chunked(gpu):
+    """I=128, H=256, B=16, T=4096 as 8 chunks of 512 carrying h (no detach),
+    h0 ~ 0.5 N(0,1), 5% of [B,T] rows of x scaled x10: the same chunked run
+    through torch.nn.GRU fp32 on the GPU."""
+    print("config5 chunked vs torch chunked", flush=True)
+    c = _config5_inputs()
+    res, _ = _torch_reference(gpu, c["L"], c["I"], c["H"], c["B"], c["T"], seed=c["seed"], h0_scale=c["h0_scale"],
+                              x_hook=c["x_hook"], chunks=8)
     _assert_parity(res, "c5")
+
+
+def test_config5_chunked_bptt_equals_the_full_sequence_oracle(gpu, oracle):
+    """Chunked BPTT equals full BPTT (tests/test_sequence_chunking.py:17-35 of
+    the reference): the 8 x 512 chunked run carrying h without detach (its
+    h_n handed to the next chunk's h0, the next chunk's dh0 back as this
+    chunk's d h_n) against the float64 oracle over the whole T = 4096
+    sequence in one piece, for out, h_n, dx, dh0 and every weight gradient."""
+    import os
+
+    print("config5 chunked vs the full-sequence oracle", flush=True)
+    c = _config5_inputs()
+    res, (torch_gru, x, h0, target) = _torch_reference(gpu, c["L"], c["I"], c["H"], c["B"], c["T"], seed=c["seed"],
+                                                       h0_scale=c["h0_scale"], x_hook=c["x_hook"], chunks=8)
+    tgt = target.double().numpy()
+    scale = 2.0 / tgt.size
+    ref = oracle.stack_rows_parallel(x.double().numpy(), h0.double().numpy(), _oracle_params(torch_gru, 1),
+                                     lambda y, a, b: scale * (y - tgt[a:b]), threads=min(16, os.cpu_count() or 1))
+    _assert_oracle_errors(_oracle_errors(res["ours"], ref, 1), "c5")

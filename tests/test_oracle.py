@@ -201,3 +201,35 @@ def test_row_parallel_oracle_equals_the_single_call():
     assert np.array_equal(b.dx, bp.dx) and np.array_equal(b.dh0, bp.dh0)
     for name in ("dw_ih", "dw_hh", "db_ih", "db_hh"):
         np.testing.assert_allclose(getattr(bp, name), getattr(b, name), rtol=1e-13, atol=1e-13)
+
+
+def test_row_parallel_stack_equals_the_single_stack_call():
+    """The row-parallel stack (used for the full-size two-layer check) gives
+    stack_forward_backward's per-row results exactly and its weight gradients
+    up to the grouping of the batch sum, with the output gradient formed from
+    each chunk's own forward result (here the MSE gradient against a target),
+    and matches the committed two-layer torch.nn.GRU fixture."""
+    from oracle import gru_oracle
+
+    c = _case("two_layer")
+    L = int(c["dims"][0])
+    params = _params(c, L)
+    dy = c["dy"]
+    ref = gru_oracle.stack_forward_backward(c["x"], c["h0"], params, dy, c["dhn"])
+    par = gru_oracle.stack_rows_parallel(c["x"], c["h0"], params, lambda y, a, b: dy[a:b], threads=2,
+                                         dhn=c["dhn"])
+    assert np.array_equal(ref.y, par.y) and np.array_equal(ref.hn, par.hn)
+    assert np.array_equal(ref.dx, par.dx) and np.array_equal(ref.dhx, par.dhx)
+    for l in range(L):
+        for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh"):
+            np.testing.assert_allclose(par.grads[l][n], ref.grads[l][n], rtol=1e-13, atol=1e-13)
+            np.testing.assert_allclose(par.grads[l][n], c[f"grad_{n}_l{l}"], rtol=0, atol=1e-11)
+    np.testing.assert_allclose(par.y, c["y"], rtol=0, atol=1e-12)
+    # an output gradient that depends on the chunk's forward output
+    rng = np.random.default_rng(3)
+    target = rng.standard_normal(ref.y.shape)
+    scale = 2.0 / target.size
+    mse = gru_oracle.stack_rows_parallel(c["x"], c["h0"], params, lambda y, a, b: scale * (y - target[a:b]),
+                                         threads=3)
+    full = gru_oracle.stack_forward_backward(c["x"], c["h0"], params, scale * (mse.y - target))
+    assert np.array_equal(full.dx, mse.dx) and np.array_equal(full.dhx, mse.dhx)
