@@ -46,15 +46,14 @@ METRIC = "fp32 GRU fwd+bwd timesteps/sec & µs/step, H=256 B=64 T=512, 1 MI355X"
 B, T, I, H, L = 64, 512, 256, 256, 1
 SEED = 42
 MFMA_FP32_PEAK_TFLOPS = 157.3
-VALU_FP32_PEAK_TFLOPS = 78.6   # non-packed fp32 FMA (packed fp32 is disabled in this build)
+# Non-packed fp32 VALU FMA peak: 16 lanes per SIMD per clock (a wave64
+# v_fmac_f32 in four clocks), 1024 SIMDs at 2.4 GHz.  The published 157.3
+# TFLOP/s vector figure needs packed fp32, which this build does not use.
+# Measured on MI355X: 1.44-1.51 ns per v_fmac_f32 per SIMD with twelve
+# independent chains, 1.8 ns in the four-row forward recurrence's FMA phase.
+VALU_FP32_PEAK_TFLOPS = 78.6
 HBM_PEAK_GBS = 8000.0
-# Measured floor of the recurrences' step structure at c2, microseconds per
-# timestep: a timing copy of each kernel that keeps the exchange, both
-# barriers, the LDS broadcasts and reductions and the gate math but drops the
-# W_hh FMAs and the owner's per-step output stores and input loads (MI355X,
-# mean of two runs: forward 0.3333 / 0.3292 ms, backward 0.3499 / 0.3486 ms
-# per T = 512 launch).  The timing copy is not shipped.
-STEP_FLOOR_US = {"forward_recurrence": 0.647, "backward_recurrence": 0.682}
+RECURRENCES = ("forward_recurrence", "backward_recurrence")
 CPU_THREAD_CAP = 16  # the GPU box's CPU share for one GPU, whatever os.cpu_count() reports
 
 
@@ -410,6 +409,10 @@ def main():
     t_step, t_event_median = time_steps(ours, x, h0, target, args.steps, 2, sync, loss_fn=mse_loss)
     check_recurrences()  # raises if a recurrence call aborted
 
+    # the exchange the recurrences step with, measured live: 128 workgroup
+    # pairs (every CU busy), eight polling wavefronts each
+    exch = _lib.measure_exchange_latency(pairs=128, iters=2000)
+
     # per-step stage totals; a stage may run as several launches per step
     # (the backward recurrence in time chunks), and side-stream GEMM stages
     # overlap the recurrence, so the stages can sum to more than the step
@@ -420,6 +423,11 @@ def main():
     per_launch = max(launches[dominant], 1.0)
     dom_ms = stage_step[dominant] / per_launch           # mean launch duration
     achieved = flops[dominant] / per_launch / (dom_ms * 1e-3) / 1e12 if dom_ms > 0 else 0.0
+    # the step floor of a recurrence: one exchange one way, then the FMAs of
+    # the other slices' W_hh columns (H - 64 of the H per gate row and batch
+    # row; 64 units per workgroup) at the VALU peak over the whole GPU
+    remote_flops = 2.0 * B * 3 * H * max(H - 64, 0)
+    floor_us = exch["round_trip_ns"] / 2 * 1e-3 + remote_flops / (VALU_FP32_PEAK_TFLOPS * 1e12) * 1e6
     alg_bytes = stage_bytes(B, T, I, H).get(dominant)
     if alg_bytes:
         alg_bytes /= per_launch
@@ -449,7 +457,7 @@ def main():
         "launches_per_step": {k: round(v, 2) for k, v in launches.items()},
         "roofline": {
             "kernel": dominant,
-            "bound": "latency" if dominant in STEP_FLOOR_US else "mfma",
+            "bound": "latency" if dominant in RECURRENCES else "mfma",
             "achieved": achieved,
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
@@ -458,13 +466,17 @@ def main():
             "note": ("serial recurrence: VALU FMAs (no MFMA) between one cross-workgroup exchange per timestep, "
                      "latency-bound; achieved = algorithmic FLOPs / mean launch time from hipEvents on the launch "
                      "stream; frac against the published fp32 peak, valu_frac against the non-packed fp32 VALU "
-                     "peak, floor_frac = measured step-structure floor / measured step; traffic = copy-calibrated "
+                     "peak; floor = one exchange (half the measured ping-pong round trip) + the FMAs that need "
+                     "the exchanged values (the other slices' share of W_hh h) at the VALU peak, both measured or "
+                     "computed in this run; floor_frac = floor / measured step; traffic = copy-calibrated "
                      "FETCH_SIZE+WRITE_SIZE bytes per launch from the committed rocprofv3 summary"),
             "valu_peak": VALU_FP32_PEAK_TFLOPS,
             "valu_frac": achieved / VALU_FP32_PEAK_TFLOPS,
-            "floor_us_per_timestep": STEP_FLOOR_US.get(dominant),
-            "floor_frac": (STEP_FLOOR_US[dominant] / (stage_step[dominant] * 1e3 / T / per_launch))
-            if dominant in STEP_FLOOR_US else None,
+            "exchange_round_trip_ns": exch["round_trip_ns"],
+            "exchange_pairs_on_one_xcd": exch["same_xcd"],
+            "floor_us_per_timestep": floor_us,
+            "floor_frac": (floor_us / (stage_step[dominant] * 1e3 / T / per_launch))
+            if dominant in RECURRENCES else None,
             "us_per_timestep": stage_step[dominant] * 1e3 / T,
             "launch_ms": dom_ms,
             "launches_per_step": per_launch,

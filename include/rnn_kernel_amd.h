@@ -257,6 +257,22 @@ int rka_describe_recurrence(int dir, int batch, int hidden_size, int* out, int n
 int rka_eval_gate_functions(const float* x, float* sigmoid_out, float* tanh_out, int n, void* stream);
 
 /*
+ * Measurement of the exchange the persistent recurrences step with (for
+ * bench.py's roofline; no counterpart in the reference, whose recurrences
+ * step with cooperative grid barriers, a100_gru_h256_kernels.cu:698-778).
+ * `pairs` pairs of workgroups (eight wavefronts each, all polling; the two
+ * sides of a pair eight block ids apart, so on one XCD) ping-pong a 64-bit
+ * word `iters` times: plain store to publish, agent-scope loads to poll, as
+ * the recurrences do.  Writes the mean round trip in ns and whether every
+ * pair ran on one XCD.  Synchronous (it waits for the device and copies the
+ * timings back); every wait is bounded and one that gives up is an error.
+ * The workspace is device memory of rka_exchange_probe_workspace_bytes(pairs).
+ */
+size_t rka_exchange_probe_workspace_bytes(int pairs);
+int rka_measure_exchange_latency(int pairs, int iters, void* workspace, size_t workspace_bytes,
+                                 double* round_trip_ns, int* same_xcd);
+
+/*
  * Stage profiler (the native counterpart of the reference's per-phase CUDA
  * events, rnn_benchmark.py:642-694).  While enabled, every stage launch of
  * rka_gru_forward / rka_gru_backward is bracketed by a pair of hipEvents on

@@ -41,6 +41,8 @@ SIGNATURES = {
     "rka_set_stall_block": (_I, [_I]),
     "rka_describe_recurrence": (_I, [_I, _I, _I, ctypes.POINTER(_I), _I]),
     "rka_eval_gate_functions": (_I, [_P, _P, _P, _I, _P]),
+    "rka_exchange_probe_workspace_bytes": (_SZ, [_I]),
+    "rka_measure_exchange_latency": (_I, [_I, _I, _P, _SZ, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "rka_profile_enable": (_I, [_I]),
     "rka_profile_read": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "rka_profile_stage_name": (ctypes.c_char_p, [_I]),
@@ -164,3 +166,18 @@ def recurrence_abort_count() -> int:
     check(load().rka_recurrence_abort_count(ctypes.byref(n)), "rka_recurrence_abort_count")
     return int(n.value)
 
+
+def measure_exchange_latency(pairs: int = 128, iters: int = 2000) -> dict:
+    """Mean round trip (ns) of the recurrences' cross-workgroup exchange,
+    measured by a ping-pong of `pairs` workgroup pairs on the current device;
+    see rka_measure_exchange_latency."""
+    import torch
+
+    lib = load()
+    nbytes = lib.rka_exchange_probe_workspace_bytes(pairs)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    rt = ctypes.c_double(0.0)
+    same = ctypes.c_int(0)
+    check(lib.rka_measure_exchange_latency(pairs, iters, ws.data_ptr(), nbytes, ctypes.byref(rt), ctypes.byref(same)),
+          "rka_measure_exchange_latency")
+    return {"round_trip_ns": rt.value, "same_xcd": bool(same.value), "pairs": pairs, "iters": iters}

@@ -986,3 +986,16 @@ def test_config5_chunked_bptt_equals_the_full_sequence_oracle(gpu, oracle):
     ref = oracle.stack_rows_parallel(x.double().numpy(), h0.double().numpy(), _oracle_params(torch_gru, 1),
                                      lambda y, a, b: scale * (y - tgt[a:b]), threads=min(16, os.cpu_count() or 1))
     _assert_oracle_errors(_oracle_errors(res["ours"], ref, 1), "c5")
+
+
+def test_exchange_latency_probe(gpu, hip_lib):
+    """The committed exchange measurement bench.py reports: one pair and
+    every CU busy (128 pairs); both sides of each pair on one XCD, round
+    trips finite and within the range such an exchange takes (0.1 - 10 us)."""
+    from rnn_kernel_amd import _lib
+
+    for pairs in (1, 128):
+        r = _lib.measure_exchange_latency(pairs=pairs, iters=500)
+        print("exchange probe", r, flush=True)
+        assert r["same_xcd"]
+        assert 100.0 < r["round_trip_ns"] < 10000.0

@@ -73,6 +73,9 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     out = (ctypes.c_int * 2)()
     assert hip_lib.rka_describe_recurrence(0, 4, 16, out, 0) == 1001  # n_out must be >= 1
     assert hip_lib.rka_describe_recurrence(2, 4, 16, out, 2) == 1001  # bad direction
+    rt, same = ctypes.c_double(0), ctypes.c_int(0)
+    assert hip_lib.rka_measure_exchange_latency(0, 10, None, 0, ctypes.byref(rt), ctypes.byref(same)) == 1001
+    assert hip_lib.rka_exchange_probe_workspace_bytes(0) == 0 and hip_lib.rka_exchange_probe_workspace_bytes(128) > 0
     assert hip_lib.rka_set_gemm_tiles(2) == 1001
     assert hip_lib.rka_set_gemm_tiles(-1) == 1001
     assert hip_lib.rka_set_gemm_tiles(1) == 0 and hip_lib.rka_set_gemm_tiles(0) == 0
