@@ -507,6 +507,287 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
     }
 }
 
+// ------------------------------------------------- forward, four rows ---
+// Forward recurrence with four batch rows per workgroup on the matrix cores
+// (v_mfma_f32_4x4x1_16b_f32).  With four rows the W_hh product of a step is
+// a [64 units x 3 gates] x k x [4 rows] block per workgroup, and the 4x4x1
+// MFMA fills all of it: block b of the sixteen takes units 4 b .. 4 b + 3, its
+// four columns the four rows, so one instruction is 64 units x 4 rows of one
+// k and gate (256 multiply-adds).  Measured on MI355X it issues one per 4.1 ns
+// per SIMD in this loop shape (two wavefronts per SIMD, three accumulators),
+// against 1.4-1.8 ns per 64-lane v_fmac_f32, i.e. 1.4x the rate of the VALU
+// FMAs, which bound the four-row step (a wavefront issuing MFMAs and one
+// issuing VALU FMAs on the same SIMD do not overlap).
+// Lane l of every wavefront is unit 64 s + l (MFMA A row l % 4 of block l / 4)
+// and holds, for each slot j (slot 0 = the workgroup's own slice, then the
+// others in rotation), the three gates' W_hh at the eight k =
+// 64 ((s + j) mod S) + 8 w + c, c < 8 (24 S VGPRs).  The B operand of k is
+// h_{t-1}[row l % 4][k] in lane l, read from LDS four k at a time.  A
+// wavefront's D registers hold its k's share of the gate sums, D[g] reg r of
+// lane l being unit 4 (l / 4) + r of row l % 4; the eight shares meet in LDS
+// and the owner of row r (wavefront r) adds them in a fixed tree.  The
+// exchange, its words and tags, the owners' gate math, outputs and failure
+// handling are those of gru_fwd_local_kernel with four rows.
+template <int S>
+__global__ __launch_bounds__(NTH) void gru_fwd_mfma4_kernel(
+    const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
+    const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
+    float* __restrict__ reserve, unsigned long long* __restrict__ exch, int* __restrict__ abort_flag,
+    RegParams p) {
+    constexpr int R = 4;
+    constexpr int NR = S - 1;        // remote slots
+    constexpr int WE = 32 * NR;      // polled words per wavefront: (slot, c, row)
+    constexpr int NPR = WE > 64 ? 2 : 1;  // poll registers per lane
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) float part[2][NW][3][R][64];  // [parity][wave][gate][row][unit]
+    __shared__ __attribute__((aligned(16))) float hloc[2][R][64];          // [parity][row][unit]
+    __shared__ __attribute__((aligned(16))) float hrem[NW][NR > 0 ? NR : 1][R][8];  // per wave: [slot][row][c]
+    __shared__ int s_abort;
+    __shared__ int s_local;
+
+    const int B = p.B, T = p.T, H = p.H;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const rec::GroupCoords gc = rec::group_coords(p.S);
+    if (gc.g >= p.G) return;  // padding workgroup of a grid rounded up to whole XCDs
+    const int s = gc.s;
+    const int row0 = gc.g * R;
+    const int u = s * 64 + lane;  // this lane's unit (A row, owner unit)
+    const bool uvalid = u < H;
+    const int lrow = lane & 3;    // this lane's B column / D column: row lrow
+    auto kof = [&](int j, int c) { return 64 * ((s + j) % S) + 8 * wave + c; };
+
+    // A operands: wa[g][8 j + c] = W_hh[g H + u][kof(j, c)] (0 past H)
+    float wa[3][8 * S];
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int k = kof(j, c);
+            const bool ok = uvalid && k < H;
+#pragma unroll
+            for (int g = 0; g < 3; ++g) wa[g][8 * j + c] = ok ? w_hh[((size_t)g * H + u) * H + k] : 0.f;
+        }
+
+    // wave r < R owns row row0 + r: its gate math, outputs and exchange words
+    const int orow = row0 + (wave < R ? wave : 0);
+    const bool owner = wave < R && uvalid && orow < B;
+    float h_prev = 0.f, bias_r = 0.f, bias_z = 0.f, bias_n = 0.f;
+    float gxs[2][3];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) gxs[e][c] = 0.f;
+    const float* gx_row = gx + (size_t)orow * T * 3 * H + u;
+    auto load_gx = [&](float (&d)[3], int t) {
+        const float* gp = gx_row + (size_t)t * 3 * H;
+        d[0] = gp[0];
+        d[1] = gp[H];
+        d[2] = gp[2 * H];
+    };
+    if (owner) {
+        h_prev = h0[(size_t)orow * H + u];
+        bias_r = b_hh[u];
+        bias_z = b_hh[H + u];
+        bias_n = b_hh[2 * H + u];
+        load_gx(gxs[0], 0);
+    }
+    if (threadIdx.x == 0) s_abort = 0;
+    const rec::WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
+    const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
+
+    // Polled word e of the wavefront: remote slot 1 + e / 32, c = (e / 4) % 8,
+    // row e % 4; lane l polls e = l and (S = 4) e = 64 + l.  A word whose k is
+    // past H re-reads the wavefront's first valid word (word 0 when none); a
+    // row past B reads the group's first row.
+    bool rvalid[R];
+    unsigned roff[R];  // word offset of row r within a slot (B H < 2^29)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rvalid[r] = row0 + r < B;
+        roff[r] = (unsigned)(rvalid[r] ? row0 + r : row0) * (unsigned)H;
+    }
+    int fallback = -1;
+#pragma unroll
+    for (int e = 0; e < WE; e += 4) {
+        const int k = kof(1 + e / 32, (e / 4) % 8);
+        if (fallback < 0 && k < H) fallback = k;
+    }
+    if (fallback < 0) fallback = 0;
+    unsigned poff[NPR];
+    bool pval[NPR];
+#pragma unroll
+    for (int v = 0; v < NPR; ++v) {
+        const int e = 64 * v + lane;
+        const bool in = e < WE;
+        const int k = in ? kof(1 + e / 32, (e / 4) % 8) : H;
+        const int r = e & 3;
+        pval[v] = in && k < H && rvalid[r];
+        poff[v] = (pval[v] ? roff[r] : roff[0]) + (unsigned)(k < H ? k : fallback);
+    }
+
+    const int pub_flip = (int)blockIdx.x == p.stall_block ? 1 : 0;
+    const unsigned slot_words = (unsigned)B * (unsigned)H, my_word = (unsigned)orow * (unsigned)H + (unsigned)u;
+    const unsigned pub_off[2] = {(unsigned)pub_flip * slot_words + my_word,
+                                 (unsigned)(1 - pub_flip) * slot_words + my_word};
+    float o_h = 0.f, o_r = 0.f, o_z = 0.f, o_n = 0.f, o_a = 0.f;
+    float* y_row = y + (size_t)orow * T * H + u;
+    float* res_row = reserve ? reserve + (size_t)orow * T * 4 * H + 4 * u : nullptr;
+    auto store_outputs = [&](int t) {
+        y_row[(size_t)t * H] = o_h;
+        if (res_row) *reinterpret_cast<float4*>(res_row + (size_t)t * 4 * H) = make_float4(o_r, o_z, o_n, o_a);
+    };
+
+    f4 acc[3];
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int g = 0; g < 3; ++g) acc[g] = f4{0.f, 0.f, 0.f, 0.f};
+    };
+    // slot j's eight k with the B operands hb[c] = h[row lrow][kof(j, c)]
+    auto mfma8 = [&](const float (&hb)[8], int j) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+                acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(wa[g][8 * j + c], hb[c], acc[g], 0, 0, 0);
+    };
+    auto lds8 = [](const float* src, float (&hv)[8]) {
+        const float4 a = *reinterpret_cast<const float4*>(src);
+        const float4 b = *reinterpret_cast<const float4*>(src + 4);
+        hv[0] = a.x; hv[1] = a.y; hv[2] = a.z; hv[3] = a.w;
+        hv[4] = b.x; hv[5] = b.y; hv[6] = b.z; hv[7] = b.w;
+    };
+    // own slot of the next step from the owners' h in LDS
+    auto local_mfmas = [&](int par) {
+        zero_acc();
+        float hb[8];
+        lds8(&hloc[par][lrow][8 * wave], hb);
+        mfma8(hb, 0);
+    };
+    unsigned long long first_read[NPR];
+#pragma unroll
+    for (int v = 0; v < NPR; ++v) first_read[v] = 0;
+    // step 0's own slot from h0
+    {
+        zero_acc();
+        float hb[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int k = kof(0, c);
+            hb[c] = k < H && rvalid[lrow] ? h0[roff[lrow] + k] : 0.f;
+        }
+        mfma8(hb, 0);
+    }
+
+    auto step = [&](int t, const float (&cur)[3], float (&nxt)[3]) -> bool {
+        // @probe:step_begin
+        if constexpr (NR > 0) {
+            float hx[NPR];
+            if (t == 0) {
+#pragma unroll
+                for (int v = 0; v < NPR; ++v) {
+                    const int e = 64 * v + lane;
+                    hx[v] = pval[v] ? h0[poff[v] - roff[e & 3] + (unsigned)(row0 + (e & 3)) * (unsigned)H] : 0.f;
+                }
+            } else {
+                const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H;
+                const unsigned long long* pp[NPR];
+#pragma unroll
+                for (int v = 0; v < NPR; ++v) pp[v] = src + poff[v];
+                bool ok = true;
+                rec::wait_words<NPR, true>(pp, pval, first_read, (unsigned)t, wc, ok);
+#pragma unroll
+                for (int v = 0; v < NPR; ++v) hx[v] = pval[v] ? __uint_as_float((unsigned)first_read[v]) : 0.f;
+                if (!ok) s_abort = 1;
+            }
+            // word e to hrem[wave][slot e / 32][row e % 4][c (e / 4) % 8]
+#pragma unroll
+            for (int v = 0; v < NPR; ++v) {
+                const int e = 64 * v + lane;
+                if (e < WE) hrem[wave][e / 32][e & 3][(e / 4) & 7] = hx[v];
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (owner) {
+            if (t > 0) store_outputs(t - 1);
+            if (t + 1 < T) load_gx(nxt, t + 1);
+        }
+        // @probe:polled
+#pragma unroll
+        for (int jj = 0; jj < NR; ++jj) {
+            float hb[8];
+            lds8(&hrem[wave][jj][lrow][0], hb);
+            mfma8(hb, jj + 1);
+        }
+        // this wavefront's shares: D[g] reg r of lane l = unit 4 (l / 4) + r, row l % 4
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+            *reinterpret_cast<float4*>(&part[t & 1][wave][g][lrow][4 * (lane >> 2)]) =
+                make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+        // @probe:computed
+        __syncthreads();
+        // @probe:synced
+        const bool abort_now = s_abort != 0;
+        if (owner) {
+            const int pb = t & 1, rr = wave;
+            auto sum8 = [&](int g) { return rec::tree8([&](int w2) { return part[pb][w2][g][rr][lane]; }); };
+            const float sr = bias_r + sum8(0);
+            const float sz = bias_z + sum8(1);
+            const float sn = bias_n + sum8(2);
+            const float r = rec::sigmoid_f(cur[0] + sr);
+            const float z = rec::sigmoid_f(cur[1] + sz);
+            const float n = rec::tanh_f(cur[2] + r * sn);
+            const float h = n + z * (h_prev - n);
+            if constexpr (NR > 0) {
+                unsigned off = pub_off[t & 1];
+                asm volatile("" : "+v"(off));
+                rec::publish_word(exch + off, rec::pack_word(h, (unsigned)(t + 1)), xlocal);
+            }
+            o_h = h;
+            o_r = r;
+            o_z = z;
+            o_n = n;
+            o_a = sn;
+            h_prev = h;
+        }
+        if (wave < R) hloc[t & 1][wave][lane] = owner ? h_prev : 0.f;  // zero past H and B
+        __syncthreads();
+        // @probe:released
+        if (t + 1 < T) {
+            if constexpr (NR > 0) {
+                const unsigned long long* src = exch + (size_t)(t & 1) * B * H;
+#pragma unroll
+                for (int v = 0; v < NPR; ++v) first_read[v] = rec::load_word(src + poff[v]);
+            }
+            local_mfmas(t & 1);
+        }
+        // @probe:step_end
+        return !abort_now;
+    };
+    int t_stop = T;
+    for (int t = 0; t < T; t += 2) {
+        if (!step(t, gxs[0], gxs[1])) {
+            t_stop = t;
+            break;
+        }
+        if (t + 1 < T && !step(t + 1, gxs[1], gxs[0])) {
+            t_stop = t + 1;
+            break;
+        }
+    }
+    // @probe:kernel_end
+    const bool aborted = t_stop < T;
+    if (owner) {
+        if (!aborted) {
+            store_outputs(T - 1);
+        } else {
+            o_h = o_r = o_z = o_n = o_a = __builtin_nanf("");
+            for (int t = t_stop; t < T; ++t) store_outputs(t);
+        }
+        hn[(unsigned)(orow * H + u)] = aborted ? __builtin_nanf("") : h_prev;
+    }
+}
+
 // ------------------------------------------------------------ backward ---
 // Transposed sum over the four 16-lane rows: given t[v] (v = 0..3) in every
 // row, returns in row r the sum of t[r] over the rows, (R0 + R2) + (R1 + R3).
@@ -919,7 +1200,7 @@ const void* local_ptr(int dir, int rows, bool io) {
             return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true>)
                       : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false>);
         case 2: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 2, false>);
-        default: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 4, false>);
+        default: return reinterpret_cast<const void*>(&gru_fwd_mfma4_kernel<S>);
     }
 }
 
