@@ -46,12 +46,10 @@ METRIC = "fp32 GRU fwd+bwd timesteps/sec & µs/step, H=256 B=64 T=512, 1 MI355X"
 B, T, I, H, L = 64, 512, 256, 256, 1
 SEED = 42
 MFMA_FP32_PEAK_TFLOPS = 157.3
-# Non-packed fp32 VALU FMA peak: 16 lanes per SIMD per clock (a wave64
-# v_fmac_f32 in four clocks), 1024 SIMDs at 2.4 GHz.  The published 157.3
-# TFLOP/s vector figure needs packed fp32, which this build does not use.
-# Measured on MI355X: 1.44-1.51 ns per v_fmac_f32 per SIMD with twelve
-# independent chains, 1.8 ns in the four-row forward recurrence's FMA phase.
-VALU_FP32_PEAK_TFLOPS = 78.6
+# The recurrences' FMAs are non-packed v_fmac_f32 (this build disables packed
+# fp32); the published 157.3 TFLOP/s vector figure assumes packed FMAs.  Their
+# roof is measured in each run (rka_measure_fma_rate: every CU issuing
+# independent FMA chains), and valu_frac and the step floor use that rate.
 HBM_PEAK_GBS = 8000.0
 RECURRENCES = ("forward_recurrence", "backward_recurrence")
 CPU_THREAD_CAP = 16  # the GPU box's CPU share for one GPU, whatever os.cpu_count() reports
@@ -412,6 +410,9 @@ def main():
     # the exchange the recurrences step with, measured live: 128 workgroup
     # pairs (every CU busy), eight polling wavefronts each
     exch = _lib.measure_exchange_latency(pairs=128, iters=2000)
+    # the non-packed fp32 FMA issue rate, measured live on every CU
+    fma = _lib.measure_fma_rate()
+    valu_peak = fma["tflops"]
 
     # per-step stage totals; a stage may run as several launches per step
     # (the backward recurrence in time chunks), and side-stream GEMM stages
@@ -425,9 +426,9 @@ def main():
     achieved = flops[dominant] / per_launch / (dom_ms * 1e-3) / 1e12 if dom_ms > 0 else 0.0
     # the step floor of a recurrence: one exchange one way, then the FMAs of
     # the other slices' W_hh columns (H - 64 of the H per gate row and batch
-    # row; 64 units per workgroup) at the VALU peak over the whole GPU
+    # row; 64 units per workgroup) at the measured FMA rate over the whole GPU
     remote_flops = 2.0 * B * 3 * H * max(H - 64, 0)
-    floor_us = exch["round_trip_ns"] / 2 * 1e-3 + remote_flops / (VALU_FP32_PEAK_TFLOPS * 1e12) * 1e6
+    floor_us = exch["round_trip_ns"] / 2 * 1e-3 + remote_flops / (valu_peak * 1e12) * 1e6
     alg_bytes = stage_bytes(B, T, I, H).get(dominant)
     if alg_bytes:
         alg_bytes /= per_launch
@@ -465,13 +466,14 @@ def main():
             "traffic": measured_traffic(dominant),
             "note": ("serial recurrence: VALU FMAs (no MFMA) between one cross-workgroup exchange per timestep, "
                      "latency-bound; achieved = algorithmic FLOPs / mean launch time from hipEvents on the launch "
-                     "stream; frac against the published fp32 peak, valu_frac against the non-packed fp32 VALU "
-                     "peak; floor = one exchange (half the measured ping-pong round trip) + the FMAs that need "
-                     "the exchanged values (the other slices' share of W_hh h) at the VALU peak, both measured or "
+                     "stream; frac against the published fp32 peak, valu_frac against the non-packed fp32 FMA "
+                     "issue rate measured in this run; floor = one exchange (half the measured ping-pong round trip) + the FMAs that need "
+                     "the exchanged values (the other slices' share of W_hh h) at that FMA rate, both measured or "
                      "computed in this run; floor_frac = floor / measured step; traffic = copy-calibrated "
                      "FETCH_SIZE+WRITE_SIZE bytes per launch from the committed rocprofv3 summary"),
-            "valu_peak": VALU_FP32_PEAK_TFLOPS,
-            "valu_frac": achieved / VALU_FP32_PEAK_TFLOPS,
+            "valu_peak": valu_peak,
+            "valu_frac": achieved / valu_peak,
+            "fma_ns_per_instruction_per_simd": fma["ns_per_instruction"],
             "exchange_round_trip_ns": exch["round_trip_ns"],
             "exchange_pairs_on_one_xcd": exch["same_xcd"],
             "floor_us_per_timestep": floor_us,

@@ -273,6 +273,18 @@ int rka_measure_exchange_latency(int pairs, int iters, void* workspace, size_t w
                                  double* round_trip_ns, int* same_xcd);
 
 /*
+ * Measurement of the issue rate of non-packed fp32 FMAs (v_fmac_f32 with
+ * VGPR operands, the form of the recurrences' W_hh products; for bench.py's
+ * roofline, no counterpart in the reference).  Every CU runs one or two
+ * 512-thread workgroups whose lanes advance 12 or 24 independent FMA chains;
+ * writes the best of the four configurations as ns per wave64 instruction
+ * per SIMD and as TFLOP/s over the device.  Synchronous.  The workspace is
+ * device memory of rka_fma_probe_workspace_bytes() (0 if no device).
+ */
+size_t rka_fma_probe_workspace_bytes(void);
+int rka_measure_fma_rate(void* workspace, size_t workspace_bytes, double* ns_per_instruction, double* tflops);
+
+/*
  * Stage profiler (the native counterpart of the reference's per-phase CUDA
  * events, rnn_benchmark.py:642-694).  While enabled, every stage launch of
  * rka_gru_forward / rka_gru_backward is bracketed by a pair of hipEvents on

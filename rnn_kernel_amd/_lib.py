@@ -43,6 +43,8 @@ SIGNATURES = {
     "rka_eval_gate_functions": (_I, [_P, _P, _P, _I, _P]),
     "rka_exchange_probe_workspace_bytes": (_SZ, [_I]),
     "rka_measure_exchange_latency": (_I, [_I, _I, _P, _SZ, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
+    "rka_fma_probe_workspace_bytes": (_SZ, []),
+    "rka_measure_fma_rate": (_I, [_P, _SZ, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "rka_profile_enable": (_I, [_I]),
     "rka_profile_read": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
     "rka_profile_stage_name": (ctypes.c_char_p, [_I]),
@@ -181,3 +183,19 @@ def measure_exchange_latency(pairs: int = 128, iters: int = 2000) -> dict:
     check(lib.rka_measure_exchange_latency(pairs, iters, ws.data_ptr(), nbytes, ctypes.byref(rt), ctypes.byref(same)),
           "rka_measure_exchange_latency")
     return {"round_trip_ns": rt.value, "same_xcd": bool(same.value), "pairs": pairs, "iters": iters}
+
+
+def measure_fma_rate() -> dict:
+    """Issue rate of non-packed fp32 FMAs on the current device (ns per wave64
+    instruction per SIMD, TFLOP/s over the device); see rka_measure_fma_rate."""
+    import torch
+
+    lib = load()
+    nbytes = lib.rka_fma_probe_workspace_bytes()
+    if nbytes == 0:
+        raise RuntimeError("rka_fma_probe_workspace_bytes: no device")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    ns = ctypes.c_double(0.0)
+    tf = ctypes.c_double(0.0)
+    check(lib.rka_measure_fma_rate(ws.data_ptr(), nbytes, ctypes.byref(ns), ctypes.byref(tf)), "rka_measure_fma_rate")
+    return {"ns_per_instruction": ns.value, "tflops": tf.value}

@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "librnn_kernel_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ["rka_capi.hip", "gemm_f32.hip", "gru_recurrence.hip", "gru_rec_tiled.hip", "gru_rec_reg.hip",
-           "train_ops.hip", "probe_exchange.hip"]
+           "train_ops.hip", "probes.hip"]
 ARCH = "gfx950"
 
 

@@ -1,11 +1,16 @@
-// Measurement of the cross-workgroup exchange the persistent recurrences are
-// built on (bench.py reports it beside each recurrence's step time): a
-// ping-pong between pairs of workgroups on one XCD, each side publishing a
-// 64-bit tagged word with a plain store and polling its partner's with
-// agent-scope loads, exactly as the recurrence kernels exchange h_t / G_h,t.
-// Every workgroup has eight wavefronts that all poll (as the recurrences'
-// do), and `pairs` pairs run at once (128 pairs: every CU of an MI355X
-// busy).  Waits are bounded; a wait that gives up is reported, not hidden.
+// Measurements of the two hardware rates the persistent recurrences' step is
+// built from (bench.py reports both beside each recurrence's step time):
+//
+// - the cross-workgroup exchange: a ping-pong between pairs of workgroups on
+//   one XCD, each side publishing a 64-bit tagged word with a plain store and
+//   polling its partner's with agent-scope loads, exactly as the recurrence
+//   kernels exchange h_t / G_h,t.  Every workgroup has eight wavefronts that
+//   all poll (as the recurrences' do), and `pairs` pairs run at once (128
+//   pairs: every CU of an MI355X busy).  Waits are bounded; a wait that gives
+//   up is reported, not hidden;
+// - the issue rate of non-packed fp32 FMAs (v_fmac_f32 with VGPR operands,
+//   the recurrences' W_hh products): every CU runs 512-thread workgroups whose
+//   lanes each advance independent FMA chains.
 #include "rka_internal.h"
 
 #include <algorithm>
@@ -70,6 +75,42 @@ __global__ void zero_words_kernel(unsigned long long* __restrict__ w, size_t n) 
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) w[i] = 0;
 }
 
+// C independent accumulators a <- h * w + a per lane (v_fmac_f32, every
+// operand a VGPR, as in the recurrences' W_hh products), 8 C FMAs per
+// iteration; h and w are per-lane values near 1e-3 and 0.5, so no sum
+// overflows or goes subnormal.  ticks[2 b] / ticks[2 b + 1] = 100 MHz clock
+// at the start and end of block b, each taken after a barrier; out keeps the
+// sums live.
+template <int C>
+__global__ __launch_bounds__(512) void fma_rate_kernel(float* __restrict__ out, long long* __restrict__ ticks,
+                                                       int iters, float w0, float h0) {
+    const float lanef = (float)(threadIdx.x & 63);
+    const float w = w0 + 1e-6f * lanef;
+    float h[4], a[C];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) h[q] = h0 * (float)(q + 1) + 1e-7f * lanef;
+#pragma unroll
+    for (int c = 0; c < C; ++c) a[c] = 0.f;
+    __syncthreads();
+    const long long t0 = __builtin_amdgcn_s_memrealtime();
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int c = 0; c < C; ++c) a[c] = fmaf(h[(r + c) & 3], w, a[c]);
+    }
+    __syncthreads();
+    const long long t1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) s += a[c];
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+    if (threadIdx.x == 0) {
+        ticks[2 * blockIdx.x] = t0;
+        ticks[2 * blockIdx.x + 1] = t1;
+    }
+}
+
 }  // namespace
 }  // namespace rka
 
@@ -126,5 +167,69 @@ extern "C" int rka_measure_exchange_latency(int pairs, int iters, void* workspac
     // s_memrealtime counts at 100 MHz: 10 ns per tick
     *round_trip_ns = n ? sum / n * 10.0 / iters : 0.0;
     *same_xcd = same;
+    return 0;
+}
+
+namespace {
+
+constexpr int kFmaProbeMaxBlocksPerCu = 2;
+constexpr int kFmaProbeIters = 2000;
+
+// One launch of fma_rate_kernel<C> with `per_cu` 512-thread workgroups per
+// CU (2 per_cu wavefronts per SIMD); ns per wave64 FMA instruction per SIMD.
+template <int C>
+int time_fma(const DeviceInfo& dev, int per_cu, float* out, long long* ticks, double* ns) {
+    const int blocks = dev.num_cus * per_cu;
+    hipLaunchKernelGGL(fma_rate_kernel<C>, dim3(blocks), dim3(512), 0, nullptr, out, ticks, kFmaProbeIters, 0.5f,
+                       1e-3f);
+    RKA_RETURN_IF_HIP(hipGetLastError());
+    RKA_RETURN_IF_HIP(hipDeviceSynchronize());
+    std::vector<long long> t(2 * (size_t)blocks);
+    RKA_RETURN_IF_HIP(hipMemcpy(t.data(), ticks, sizeof(long long) * t.size(), hipMemcpyDeviceToHost));
+    long long first = t[0], last = t[1];
+    for (int b = 0; b < blocks; ++b) {
+        first = std::min(first, t[2 * b]);
+        last = std::max(last, t[2 * b + 1]);
+    }
+    // per SIMD: 2 per_cu wavefronts x iters x 8 C instructions; 10 ns per tick
+    const double insts = 2.0 * per_cu * kFmaProbeIters * 8.0 * C;
+    *ns = (double)(last - first) * 10.0 / insts;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" size_t rka_fma_probe_workspace_bytes(void) {
+    const DeviceInfo* dev = nullptr;
+    if (current_device_info(&dev) != 0) return 0;
+    const size_t blocks = (size_t)dev->num_cus * kFmaProbeMaxBlocksPerCu;
+    return blocks * 512 * sizeof(float) + blocks * 2 * sizeof(long long);
+}
+
+extern "C" int rka_measure_fma_rate(void* workspace, size_t workspace_bytes, double* ns_per_instruction,
+                                    double* tflops) {
+    clear_error();
+    if (!ns_per_instruction || !tflops)
+        return fail(RKA_ERR_INVALID_ARGUMENT, "rka_measure_fma_rate: null output");
+    const DeviceInfo* dev = nullptr;
+    RKA_RETURN_IF_ERR(current_device_info(&dev));
+    const size_t need = rka_fma_probe_workspace_bytes();
+    if (!workspace || workspace_bytes < need)
+        return fail(RKA_ERR_WORKSPACE_TOO_SMALL, "rka_measure_fma_rate: workspace needs " + std::to_string(need) +
+                                                     " bytes");
+    const size_t blocks = (size_t)dev->num_cus * kFmaProbeMaxBlocksPerCu;
+    auto* out = reinterpret_cast<float*>(workspace);
+    auto* ticks = reinterpret_cast<long long*>(out + blocks * 512);
+    double ns = 0, best = 0;
+    RKA_RETURN_IF_ERR(time_fma<12>(*dev, 1, out, ticks, &ns));  // warm-up, not counted
+    for (int per_cu = 1; per_cu <= kFmaProbeMaxBlocksPerCu; ++per_cu) {
+        RKA_RETURN_IF_ERR(time_fma<12>(*dev, per_cu, out, ticks, &ns));
+        if (best == 0 || ns < best) best = ns;
+        RKA_RETURN_IF_ERR(time_fma<24>(*dev, per_cu, out, ticks, &ns));
+        if (ns < best) best = ns;
+    }
+    *ns_per_instruction = best;
+    // 64 lanes x 2 FLOP per instruction on each of the 4 SIMDs of every CU
+    *tflops = best > 0 ? 4.0 * dev->num_cus * 128.0 / best * 1e-3 : 0.0;
     return 0;
 }

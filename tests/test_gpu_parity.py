@@ -999,3 +999,16 @@ def test_exchange_latency_probe(gpu, hip_lib):
         print("exchange probe", r, flush=True)
         assert r["same_xcd"]
         assert 100.0 < r["round_trip_ns"] < 10000.0
+
+
+def test_fma_rate_probe(gpu, hip_lib):
+    """The committed FMA issue-rate measurement bench.py prices the
+    recurrences' FMAs against: a finite rate no faster than two clocks per
+    wave64 instruction at 2.4 GHz (the published 157.3 TFLOP/s) and no
+    slower than eight."""
+    from rnn_kernel_amd import _lib
+
+    r = _lib.measure_fma_rate()
+    print("fma probe", r, flush=True)
+    assert 2 / 2.4 * 0.95 < r["ns_per_instruction"] < 8 / 2.4
+    assert 20.0 < r["tflops"] < 157.3 * 1.05

@@ -76,6 +76,8 @@ def test_library_rejects_bad_arguments_without_touching_a_gpu(hip_lib):
     rt, same = ctypes.c_double(0), ctypes.c_int(0)
     assert hip_lib.rka_measure_exchange_latency(0, 10, None, 0, ctypes.byref(rt), ctypes.byref(same)) == 1001
     assert hip_lib.rka_exchange_probe_workspace_bytes(0) == 0 and hip_lib.rka_exchange_probe_workspace_bytes(128) > 0
+    ns, tf = ctypes.c_double(0), ctypes.c_double(0)
+    assert hip_lib.rka_measure_fma_rate(None, 0, None, ctypes.byref(tf)) == 1001  # null output
     assert hip_lib.rka_set_gemm_tiles(2) == 1001
     assert hip_lib.rka_set_gemm_tiles(-1) == 1001
     assert hip_lib.rka_set_gemm_tiles(1) == 0 and hip_lib.rka_set_gemm_tiles(0) == 0
