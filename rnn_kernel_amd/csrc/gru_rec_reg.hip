@@ -832,6 +832,11 @@ __device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
 // forward, with the own entries' weights in LDS to fit 168 VGPRs, measured
 // 0.50-0.51 vs 0.48 ms per c2 launch.
 //
+// PH = 2 (four rows): each step runs as two phases of two rows, so that one
+// half's exchange travels while the other half computes (c4 backward 2.32
+// vs 2.37 us per step; the step is bound by the VALU work of four rows, not
+// by the exchange).
+//
 // NWB wavefronts (8, or 16 for one row: 64 j-groups of 3 own and 3 (S - 1)
 // remote entries, one poll register per lane, 122 VGPRs at S = 4).  The
 // remote FMAs are bound by the SIMD's VALU issue rate (running them twice
@@ -839,7 +844,7 @@ __device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
 // wavefronts issue the same instructions per SIMD; measured at c2 (same
 // box, three pairs) the one-row backward took 444.2-447.0 vs 447.5-448.4
 // us per launch and the step 1.355-1.358 vs 1.361-1.364 ms.
-template <int S, int R, int NWB = NW>
+template <int S, int R, int NWB = NW, int PH = 1>
 __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
     const float* __restrict__ h0, const float* __restrict__ y, const float* __restrict__ w_hh,
@@ -847,6 +852,8 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     int* __restrict__ abort_flag, RegParams p) {
     static_assert(R == 1 || R == 2 || R == 4, "rows per workgroup");
     static_assert(NWB == 8 || NWB == 16, "wavefronts per workgroup");
+    static_assert(PH == 1 || (PH == 2 && R % 2 == 0), "phases per step");
+    constexpr int RP = R / PH;                       // rows per phase
     constexpr int NJ = 4 * NWB;                      // j-groups (sixteen-lane rows)
     constexpr int OWN = 192 / NJ;                    // own entries per j-group (6 or 3)
     constexpr int RE = OWN * (S - 1);                // remote entries per j-group
@@ -857,6 +864,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     __shared__ __attribute__((aligned(16))) float gloc[R][NJ][OWN > 4 ? 8 : 4];  // own G words by j-group
     __shared__ __attribute__((aligned(16))) float grem[NWB][R][4][GR];  // per wave and row: polled words by j-group
     __shared__ int s_abort;
+    __shared__ int s_abort2[2];  // two phases per step: by step parity
     __shared__ int s_local;
 
     const int B = p.B, T = p.T, H = p.H;
@@ -949,7 +957,10 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
         load_inputs(ins[0], T - 1 - i0);
         if (i0 + 1 < i1) load_inputs(ins[1], T - 2 - i0);
     }
-    if (threadIdx.x == 0) s_abort = 0;
+    if (threadIdx.x == 0) {
+        s_abort = 0;
+        s_abort2[0] = s_abort2[1] = 0;
+    }
     const rec::WaitCtl wc{abort_flag, p.abort_count, p.spin_limit};
     const bool xlocal = rec::group_on_one_xcd(p.xcc_words, gc.first, gc.stride, p.S, p.xcc_tag, wc, &s_local);
 
@@ -984,8 +995,8 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     // pointwise step i (t = T-1-i) from dh and its inputs: publishes G_h,t,
     // writes it to LDS by j-group, keeps the gate gradients for the store
     // after the next poll
-    auto pointwise = [&](int i, const float (&cur)[6]) {
-        if (owner) {
+    auto pointwise = [&](int i, const float (&cur)[6], bool act) {
+        if (act && owner) {
             const float gsum = dh + cur[0];
             const float cr = cur[1], cz = cur[2], cn = cur[3], ca = cur[4], hp = cur[5];
             const float dz = gsum * (hp - cn);
@@ -1003,7 +1014,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
                 rec::publish_words<3>(pp3, w3, xlocal);
             }
         }
-        if (wave < R) {
+        if (act && wave < R) {
             const float gv[3] = {owner ? o_drh : 0.f, owner ? o_dzh : 0.f, owner ? o_dan : 0.f};
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
@@ -1020,9 +1031,9 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[r][i & 1][v] = fmaf(g[i], wt[i][v], acc[r][i & 1][v]);
     };
-    auto local_fmas = [&]() {
+    auto local_fmas_rows = [&](int ra, int nr) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int r = ra; r < ra + nr; ++r) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[r][0][v] = acc[r][1][v] = 0.f;
             const float4 a = *reinterpret_cast<const float4*>(&gloc[r][J][0]);
@@ -1040,10 +1051,10 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     unsigned long long first_read[NW2 * R];
 #pragma unroll
     for (int v = 0; v < NW2 * R; ++v) first_read[v] = 0;
-    auto first_poll = [&](int i) {
+    auto first_poll_rows = [&](int i, int ra, int nr) {
         const unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int r = ra; r < ra + nr; ++r) {
             if constexpr (WE > 0) first_read[NW2 * r] = rec::load_word(slotp + roff[r] + pidx0);
             if constexpr (WE > 64) first_read[NW2 * r + 1] = rec::load_word(slotp + roff[r] + pidx1);
         }
@@ -1140,32 +1151,136 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
                 dh = ddirect + lo;
         }
         const bool more = i + 1 < i1;
-        if (more) pointwise(i + 1, nxt);
+        if (more) pointwise(i + 1, nxt, true);
         // @probe:published
         __syncthreads();
         // @probe:released
         if (more) {
-            first_poll(i + 1);
-            local_fmas();
+            first_poll_rows(i + 1, 0, R);
+            local_fmas_rows(0, R);
         }
         // @probe:step_end
         return !abort_now;
     };
-    if (i0 < i1) pointwise(i0, ins[0]);
+    // Two phases per step (PH = 2): the rows of phase 1 wait for their words,
+    // run their FMAs and reach their barrier while the words of phase 0's
+    // rows for the next step travel, and the other way round, so each
+    // half's exchange is hidden behind the other half's work.  One barrier
+    // per phase: it publishes the phase's partial sums to its owners and the
+    // other phase's own G words (written by that phase's owners after the
+    // previous barrier) to every wavefront.  Phase ra (rows ra .. ra + RP - 1)
+    // of step i; the owners are wavefronts ra .. ra + RP - 1.
+    auto phase = [&](int i, int ra, float (&cur)[6], const float (&nxt)[6]) -> bool {
+        const int t = T - 1 - i;
+        const bool mine = wave >= ra && wave < ra + RP;
+        // @probe:phase_begin
+        first_poll_rows(i, ra, RP);
+        local_fmas_rows(ra, RP);
+        float g0[GR];
+        if constexpr (WE > 0) {
+            const unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
+            const unsigned long long* pp[NW2 * RP];
+            bool pv[NW2 * RP];
+            unsigned long long fr[NW2 * RP];
+#pragma unroll
+            for (int k = 0; k < RP; ++k) {
+                const int r = ra + k;
+                pp[NW2 * k] = slotp + roff[r] + pidx0;
+                pv[NW2 * k] = pv0 && rvalid[r];
+                fr[NW2 * k] = first_read[NW2 * r];
+                if constexpr (NW2 == 2) {
+                    pp[NW2 * k + 1] = slotp + roff[r] + pidx1;
+                    pv[NW2 * k + 1] = pv1 && rvalid[r];
+                    fr[NW2 * k + 1] = first_read[NW2 * r + 1];
+                }
+            }
+            bool ok = true;
+            rec::wait_words<NW2 * RP>(pp, pv, fr, (unsigned)(i + 1), wc, ok);
+            if (!ok) s_abort2[i & 1] = 1;
+#pragma unroll
+            for (int k = 0; k < RP; ++k) {
+                const int r = ra + k;
+                const float gr0 = pv[NW2 * k] ? __uint_as_float((unsigned)fr[NW2 * k]) : 0.f;
+                if (lane < WE) grem[wave][r][lane / RE][lane % RE] = gr0;
+                if constexpr (NW2 == 2) {
+                    const float gr1 = pv[NW2 * k + 1] ? __uint_as_float((unsigned)fr[NW2 * k + 1]) : 0.f;
+                    if (lane < WE - 64) grem[wave][r][(64 + lane) / RE][(64 + lane) % RE] = gr1;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            read_grem(ra, g0);
+        }
+        // @probe:phase_polled
+        if (owner && mine) {
+            float* op = gout + ((size_t)orow * T + t) * 4 * H;  // wave-uniform
+            __builtin_nontemporal_store(o_dan, op + u);
+            __builtin_nontemporal_store(o_drh, op + H + u);
+            __builtin_nontemporal_store(o_dzh, op + 2 * H + u);
+            __builtin_nontemporal_store(o_dnh, op + 3 * H + u);
+            if (t - 2 >= p.t_begin) load_inputs(cur, t - 2);
+        }
+        if constexpr (RE > 0) {
+            fma_group(ra, g0, RE, wm);
+#pragma unroll
+            for (int k = 1; k < RP; ++k) {
+                __builtin_amdgcn_sched_barrier(0);
+                float g[GR];
+                read_grem(ra + k, g);
+                fma_group(ra + k, g, RE, wm);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < RP; ++k) {
+            const int r = ra + k;
+            float tot[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) tot[v] = acc[r][0][v] + acc[r][1][v];
+            part[i & 1][wave][r][4 * q + rho] = rows_transpose_sum(tot);
+        }
+        // @probe:phase_computed
+        __syncthreads();
+        // @probe:phase_synced
+        // every wait of step i has set its flag before the barrier of the
+        // step's last phase; the next step's waits set the other parity's
+        const bool abort_now = ra + RP == R && s_abort2[i & 1] != 0;
+        if (owner && mine) dh = ddirect + rec::tree8([&](int w2) { return part[i & 1][w2][wave][lane]; });
+        if (i + 1 < i1) pointwise(i + 1, nxt, mine);
+        // @probe:phase_end
+        return !abort_now;
+    };
+    if (i0 < i1) pointwise(i0, ins[0], true);
     __syncthreads();
-    first_poll(i0);
-    local_fmas();
     // step i stores the G row of step i: after a step that aborts, rows
     // i_stop + 1 .. i1 - 1 were not stored
     int i_stop = i1;
-    for (int i = i0; i < i1; i += 2) {
-        if (!step(i, ins[0], ins[1])) {
-            i_stop = i;
-            break;
+    if constexpr (PH == 1) {
+        first_poll_rows(i0, 0, R);
+        local_fmas_rows(0, R);
+        for (int i = i0; i < i1; i += 2) {
+            if (!step(i, ins[0], ins[1])) {
+                i_stop = i;
+                break;
+            }
+            if (i + 1 < i1 && !step(i + 1, ins[1], ins[0])) {
+                i_stop = i + 1;
+                break;
+            }
         }
-        if (i + 1 < i1 && !step(i + 1, ins[1], ins[0])) {
-            i_stop = i + 1;
-            break;
+    } else {
+        static_assert(NWB == 8, "two phases with eight wavefronts");
+        for (int i = i0; i < i1; i += 2) {
+            phase(i, 0, ins[0], ins[1]);
+            if (!phase(i, RP, ins[0], ins[1])) {
+                i_stop = i;
+                break;
+            }
+            if (i + 1 < i1) {
+                phase(i + 1, 0, ins[1], ins[0]);
+                if (!phase(i + 1, RP, ins[1], ins[0])) {
+                    i_stop = i + 1;
+                    break;
+                }
+            }
         }
     }
     // @probe:kernel_end
@@ -1192,7 +1307,7 @@ const void* local_ptr(int dir, int rows, bool io) {
         switch (rows) {
             case 1: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 1, 16>);
             case 2: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 2>);
-            default: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 4>);
+            default: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 4, NW, 2>);
         }
     }
     switch (rows) {

@@ -758,10 +758,12 @@ def test_recurrences_progress_beside_a_concurrent_kernel(gpu, B, H):
             assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("H,fwd_rows,bwd_rows", [(200, 2, 4), (256, 2, 2), (160, 4, 4), (64, 4, 2)])
+@pytest.mark.parametrize("H,fwd_rows,bwd_rows", [(200, 2, 4), (256, 2, 2), (160, 4, 4), (64, 4, 2), (48, 4, 4),
+                                                  (100, 2, 4)])
 def test_rows_per_workgroup_agree(gpu, hip_lib, H, fwd_rows, bwd_rows):
     """The local-slice recurrences with 2 or 4 batch rows per workgroup
-    (batch 9: the last group partly empty) give the one-row results."""
+    (batch 9: the last group partly empty; the four-row backward in two
+    phases of two rows, at one to four slices) give the one-row results."""
     from rnn_kernel_amd import GRU, _lib
 
     torch.manual_seed(H)
