@@ -995,15 +995,21 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     // pointwise step i (t = T-1-i) from dh and its inputs: publishes G_h,t,
     // writes it to LDS by j-group, keeps the gate gradients for the store
     // after the next poll
-    auto pointwise = [&](int i, const float (&cur)[6], bool act) {
+    // tsum: this step's W_hh^T G_h sum (dh_t = ddirect + tsum).  The factors
+    // that depend only on the saved activations are formed first, so the
+    // chain from the sum to the published words is one add and two
+    // multiplications.
+    auto pointwise = [&](int i, const float (&cur)[6], bool act, float tsum) {
         if (act && owner) {
-            const float gsum = dh + cur[0];
             const float cr = cur[1], cz = cur[2], cn = cur[3], ca = cur[4], hp = cur[5];
-            const float dz = gsum * (hp - cn);
-            o_dnh = gsum * (1.0f - cz) * (1.0f - cn * cn);
+            const float f_n = (1.0f - cz) * (1.0f - cn * cn);      // dn^ / g
+            const float f_r = ca * (cr * (1.0f - cr));             // dr^ / dn^
+            const float f_z = (hp - cn) * (cz * (1.0f - cz));      // dz^ / g
+            const float gsum = (ddirect + cur[0]) + tsum;          // g = dh_t + dy_t
+            o_dnh = gsum * f_n;
             o_dan = o_dnh * cr;
-            o_drh = o_dnh * ca * cr * (1.0f - cr);
-            o_dzh = dz * cz * (1.0f - cz);
+            o_drh = o_dnh * f_r;
+            o_dzh = gsum * f_z;
             ddirect = gsum * cz;
             if constexpr (RE > 0) {
                 const unsigned tag = (unsigned)(i + 1);
@@ -1143,15 +1149,17 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
         __syncthreads();
         // @probe:synced
         const bool abort_now = s_abort != 0;  // read with the partials
+        float tsum = 0.f;
         if (owner) {
             const float lo = rec::tree8([&](int w2) { return part[i & 1][w2][wave][lane]; });
             if constexpr (NWB == 16)
-                dh = ddirect + (lo + rec::tree8([&](int w2) { return part[i & 1][8 + w2][wave][lane]; }));
+                tsum = lo + rec::tree8([&](int w2) { return part[i & 1][8 + w2][wave][lane]; });
             else
-                dh = ddirect + lo;
+                tsum = lo;
+            dh = ddirect + tsum;
         }
         const bool more = i + 1 < i1;
-        if (more) pointwise(i + 1, nxt, true);
+        if (more) pointwise(i + 1, nxt, true, tsum);
         // @probe:published
         __syncthreads();
         // @probe:released
@@ -1243,12 +1251,16 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
         // every wait of step i has set its flag before the barrier of the
         // step's last phase; the next step's waits set the other parity's
         const bool abort_now = ra + RP == R && s_abort2[i & 1] != 0;
-        if (owner && mine) dh = ddirect + rec::tree8([&](int w2) { return part[i & 1][w2][wave][lane]; });
-        if (i + 1 < i1) pointwise(i + 1, nxt, mine);
+        float tsum = 0.f;
+        if (owner && mine) {
+            tsum = rec::tree8([&](int w2) { return part[i & 1][w2][wave][lane]; });
+            dh = ddirect + tsum;
+        }
+        if (i + 1 < i1) pointwise(i + 1, nxt, mine, tsum);
         // @probe:phase_end
         return !abort_now;
     };
-    if (i0 < i1) pointwise(i0, ins[0], true);
+    if (i0 < i1) pointwise(i0, ins[0], true, dh);  // dh_T = dhn (ddirect is 0)
     __syncthreads();
     // step i stores the G row of step i: after a step that aborts, rows
     // i_stop + 1 .. i1 - 1 were not stored
