@@ -139,10 +139,12 @@ int rka_gru_recurrence_forward(const float* gx, const float* h0,
  * calls this entry point; the first call on a device only looks up its
  * address there.  The call allocates no device memory.  Limit: batch * hidden_size <= 262144 (2 B H 8-byte
  * words in 4 MiB); larger shapes return RKA_ERR_UNSUPPORTED_SHAPE without
- * launching.  Every call on a GPU shares that GPU's array: calls that
- * overlap on one GPU (different streams or threads without ordering) race
- * and give wrong results; calls ordered on one stream are safe (each zeroes
- * the state it uses first). */
+ * launching; so is seq_len >= 2^24.  Every call on a GPU shares that GPU's
+ * array: calls ordered on one stream are safe (each zeroes the state it uses
+ * first); calls that overlap on one GPU (different streams or threads
+ * without ordering) race.  Each call's exchange words carry its own call
+ * number, so overlapping calls never take each other's values: they abort
+ * (NaN outputs, counted by rka_recurrence_abort_count) instead. */
 int rka_gru_recurrence_forward_noalloc(const float* gx, const float* h0,
                                        const float* w_hh, const float* b_hh,
                                        float* y, float* hn, float* reserve,

@@ -60,6 +60,7 @@ struct RegParams {
     int t_begin, t_end;  // backward: time range processed
     unsigned long long* xcc_words;  // start-up XCD check (nullable)
     unsigned xcc_tag;
+    unsigned tag_base;                    // forward: added to every step tag (rec::Args::tag_base)
     int spin_limit;                       // poll rounds before a wait gives up
     unsigned long long* abort_count;      // per-device count of aborted launches
     int stall_block;                      // test failure injection (rec::Args::stall_block)
@@ -353,7 +354,7 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
                     pv[r] = pvalid && rvalid[r];
                 }
                 bool ok = true;
-                rec::wait_words<R, R == 1>(pp, pv, first_read, (unsigned)t, wc, ok);
+                rec::wait_words<R, R == 1>(pp, pv, first_read, p.tag_base + (unsigned)t, wc, ok);
 #pragma unroll
                 for (int r = 0; r < R; ++r) hx[r] = pv[r] ? __uint_as_float((unsigned)first_read[r]) : 0.f;
                 if (!ok) s_abort = 1;
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
                 // longer fits the 256 VGPRs)
                 unsigned off = pub_off[t & 1];
                 asm volatile("" : "+v"(off));
-                rec::publish_word(exch + off, rec::pack_word(h, (unsigned)(t + 1)), xlocal);
+                rec::publish_word(exch + off, rec::pack_word(h, p.tag_base + (unsigned)(t + 1)), xlocal);
             }
             o_h = h;
             o_r = r;
@@ -695,7 +696,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_mfma4_kernel(
 #pragma unroll
                 for (int v = 0; v < NPR; ++v) pp[v] = src + poff[v];
                 bool ok = true;
-                rec::wait_words<NPR, true>(pp, pval, first_read, (unsigned)t, wc, ok);
+                rec::wait_words<NPR, true>(pp, pval, first_read, p.tag_base + (unsigned)t, wc, ok);
 #pragma unroll
                 for (int v = 0; v < NPR; ++v) hx[v] = pval[v] ? __uint_as_float((unsigned)first_read[v]) : 0.f;
                 if (!ok) s_abort = 1;
@@ -741,7 +742,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_mfma4_kernel(
             if constexpr (NR > 0) {
                 unsigned off = pub_off[t & 1];
                 asm volatile("" : "+v"(off));
-                rec::publish_word(exch + off, rec::pack_word(h, (unsigned)(t + 1)), xlocal);
+                rec::publish_word(exch + off, rec::pack_word(h, p.tag_base + (unsigned)(t + 1)), xlocal);
             }
             o_h = h;
             o_r = r;
@@ -1421,7 +1422,7 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     const bool aligned = (reinterpret_cast<uintptr_t>(a.w_hh) & 15u) == 0;
     RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
                   (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end,
-                  a.xcc_words, a.xcc_tag, a.spin_limit, a.abort_count, a.stall_block};
+                  a.xcc_words, a.xcc_tag, a.tag_base, a.spin_limit, a.abort_count, a.stall_block};
     const void* k = kernel_ptr(dir, cap, c.rows, c.slices);
     if (k == nullptr) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: no kernel for this row count");
     const unsigned blocks = (unsigned)(grid_groups(c, c.groups) * c.slices);

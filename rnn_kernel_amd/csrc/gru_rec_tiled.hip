@@ -35,6 +35,7 @@ struct RecParams {
     int t_begin, t_end;  // backward: time range processed
     unsigned long long* xcc_words;  // start-up XCD check (nullable)
     unsigned xcc_tag;
+    unsigned tag_base;                    // forward: added to every step tag (rec::Args::tag_base)
     int spin_limit;                       // poll rounds before a wait gives up
     unsigned long long* abort_count;      // per-device count of aborted launches
     int stall_block;                      // test failure injection (rec::Args::stall_block)
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
     for (int t = 0; t < T; ++t) {
         if (t > 0) {
             const unsigned long long* src = exch + (size_t)((t - 1) & 1) * B * H + (size_t)row0 * H;
-            if (!gather_rows(src, nrows, H, (unsigned)t, hl, RP, wc)) s_abort = 1;
+            if (!gather_rows(src, nrows, H, p.tag_base + (unsigned)t, hl, RP, wc)) s_abort = 1;
             __syncthreads();
         }
         float ar = 0.f, az = 0.f, an = 0.f;
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(rec::NTH) void gru_rec_forward_kernel(
             const float n = tanh_f(gxn + r * sn);
             const float h = n + z * (h_prev - n);
             publish_word(exch + (size_t)((t & 1) ^ pub_flip) * B * H + (size_t)b * H + u,
-                         pack_word(h, (unsigned)(t + 1)), xlocal);
+                         pack_word(h, p.tag_base + (unsigned)(t + 1)), xlocal);
             const size_t bt = (size_t)b * T + t;
             y[bt * H + u] = h;
             if (reserve) *reinterpret_cast<float4*>(reserve + bt * 4 * H + 4 * u) = make_float4(r, z, n, sn);
@@ -498,6 +499,7 @@ int tiled_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t st
     prm.t_end = a.t_end;
     prm.xcc_words = a.xcc_words;
     prm.xcc_tag = a.xcc_tag;
+    prm.tag_base = a.tag_base;
     prm.spin_limit = a.spin_limit;
     prm.abort_count = a.abort_count;
     prm.stall_block = a.stall_block;

@@ -232,6 +232,21 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 std::mutex g_scratch_mutex;
 std::vector<char*> g_scratch_ptr;  // per device: device address of `scratch`
+std::vector<unsigned> g_scratch_calls;  // per device: calls so far (step-tag base)
+
+// Step-tag base of the next call on a device: the call count (1..255,
+// wrapping) in the top 8 bits, so the steps (below 2^24) of two calls
+// whose launches overlap on the shared array never share a tag.  Such calls
+// race (documented); with distinct tags the waits of each give up on words
+// the other overwrote, the calls abort (NaN outputs, the abort counter) and
+// neither returns finite values taken from the other.
+unsigned next_tag_base(int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((int)g_scratch_calls.size() <= dev) g_scratch_calls.resize(dev + 1, 0u);
+    const unsigned c = g_scratch_calls[dev] % 255u + 1u;
+    g_scratch_calls[dev] = c;
+    return c << 24;
+}
 
 int scratch_address(int dev, char** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
@@ -275,6 +290,9 @@ int launch_rec_forward_noalloc(const float* gx, const float* h0, const float* w_
                     "rka_gru_recurrence_forward_noalloc: batch * hidden_size = " + std::to_string((size_t)B * H) +
                         " exceeds the static scratch limit of " + std::to_string(kNoAllocSlotBytes / 16) +
                         " (use rka_gru_recurrence_forward with a workspace)");
+    if (T >= (1 << 24))
+        return fail(RKA_ERR_UNSUPPORTED_SHAPE, "rka_gru_recurrence_forward_noalloc: seq_len " + std::to_string(T) +
+                                                   " must stay below 2^24 (its step tags carry a call number)");
     const DeviceInfo* dev = nullptr;
     RKA_RETURN_IF_ERR(current_device_info(&dev));
     char* ptr = nullptr;
@@ -295,6 +313,7 @@ int launch_rec_forward_noalloc(const float* gx, const float* h0, const float* w_
     a.H = H;
     a.t_begin = 0;
     a.t_end = T;
+    a.tag_base = next_tag_base(dev->device);
     return launch_at(0, a, st, true, stream);
 }
 

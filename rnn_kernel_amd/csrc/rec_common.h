@@ -67,6 +67,12 @@ struct Args {
     unsigned long long* xcc_words = nullptr;
     unsigned xcc_tag = 0;
     int spin_limit = 1 << 24;                 // poll rounds before a wait gives up
+    // Forward: added to every step tag of the launch's exchange words.  Calls
+    // that share exchange memory across calls (the allocation-free forward)
+    // take a different base per call, so a word left or written by another
+    // call never matches; with a private, freshly zeroed workspace it is 0
+    // (the backward, which has no allocation-free entry point, ignores it).
+    unsigned tag_base = 0;
     // Failure injection for tests (-1: off): the workgroup with this block
     // index publishes every word into the other step-parity slot, where its
     // partners never look for it, so their waits give up deterministically.
