@@ -98,19 +98,22 @@ struct RegParams {
 // wavefront (registers or LDS-DMA, one to three steps ahead) measured 0.53
 // to 0.57 ms, while the same copies from L2-resident addresses measured
 // 0.455 ms.
-template <int S, int R, bool IO>
-__global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
+template <int S, int R, bool IO, int NWF = NW>
+__global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_kernel(
     const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
     const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
     float* __restrict__ reserve, unsigned long long* __restrict__ exch, int* __restrict__ abort_flag,
     RegParams p) {
     static_assert(R == 1 || R == 2 || R == 4, "rows per workgroup");
     static_assert(!IO || R == 1, "the I/O wavefront serves one row");
-    constexpr int NR = S - 1;              // remote slots
-    constexpr int NP = NR > 0 ? 8 * NR : 4;  // polled h values per wave half and row
-    __shared__ float part[2][4][3][R][64];  // [step parity][k quarter][gate][row][unit]
+    static_assert(NWF == 8 || (NWF == 16 && R == 1), "eight compute wavefronts, or sixteen at one row");
+    constexpr int NR = S - 1;                 // remote slots
+    constexpr int NQ = NWF / 2;               // k parts of a slot (a wave takes one for 32 units)
+    constexpr int KP = 64 / NQ, KH = KP / 2;  // k per part, per wave half
+    constexpr int NP = NR > 0 ? KH * NR : 4;  // polled h values per wave half and row
+    __shared__ float part[2][NQ][3][R][64];   // [step parity][k part][gate][row][unit]
     __shared__ __attribute__((aligned(16))) float hloc[2][R][64];
-    __shared__ __attribute__((aligned(16))) float hrem[NW][R][2][NP];  // per wave, row and half: the polled h values
+    __shared__ __attribute__((aligned(16))) float hrem[NWF][R][2][NP];  // per wave, row and half: the polled h values
     __shared__ float io_out[IO ? 2 : 1][5][64];  // IO: outputs (h, r, z, n, a_n) of a step, by step parity
     __shared__ int s_abort;
     __shared__ int s_local;
@@ -124,24 +127,24 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
     const int row0 = gc.g * R;    // the group's first batch row
     const int u = s * 64 + lane;  // the owner lane's unit
     const bool uvalid = u < H;
-    // FMA layout: wave w takes units 32 (w / 4) + l % 32 of the slice and k
-    // quarter Q = w % 4; half hf = l / 32 of the wave the eight k
-    // 64 ((s + j) mod S) + 16 Q + 8 hf + i of slot j (for every row)
-    const int hf = lane >> 5, uu = lane & 31, Q = wave & 3;
-    const int fu = 32 * (wave >> 2) + uu;  // the lane's FMA unit within the slice
+    // FMA layout: wave w takes units 32 (w / NQ) + l % 32 of the slice and k
+    // part Q = w % NQ; half hf = l / 32 of the wave the KH k
+    // 64 ((s + j) mod S) + KP Q + KH hf + i of slot j (for every row)
+    const int hf = lane >> 5, uu = lane & 31, Q = wave % NQ;
+    const int fu = 32 * (wave / NQ) + uu;  // the lane's FMA unit within the slice
     const int uf = s * 64 + fu;
     const bool ufvalid = uf < H;
-    auto kofh = [&](int half, int j, int i) { return 64 * ((s + j) % S) + 16 * Q + 8 * half + i; };
+    auto kofh = [&](int half, int j, int i) { return 64 * ((s + j) % S) + KP * Q + KH * half + i; };
     auto kof = [&](int j, int i) { return kofh(hf, j, i); };
 
     if constexpr (IO) {
-        if (wave == NW) {
+        if (wave == NWF) {
             // The I/O wavefront: lane l is unit u of row row0.  Per step t,
             // before the step's first barrier, it stores the outputs of step
             // t-1 (written to io_out by the owner before the second barrier
             // of step t-1).  It takes both barriers of every step and leaves
             // the loop when the compute wavefronts do.
-            if (threadIdx.x == NW * 64) s_abort = 0;
+            if (threadIdx.x == NWF * 64) s_abort = 0;
             const bool valid = uvalid && row0 < B;
             float* yp = y + (size_t)row0 * T * H + u;
             float* rp = reserve ? reserve + (size_t)row0 * T * 4 * H + 4 * u : nullptr;
@@ -184,13 +187,13 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
         }
     }
 
-    // slot j's W_hh entries in w?[8 j .. 8 j + 7]
-    float wr[8 * S], wz[8 * S], wn[8 * S];
+    // slot j's W_hh entries in w?[KH j .. KH j + KH - 1]
+    float wr[KH * S], wz[KH * S], wn[KH * S];
     const bool vec = p.wvec != 0;
 #pragma unroll
     for (int j = 0; j < S; ++j) {
 #pragma unroll
-        for (int i = 0; i < 8; i += 4) {
+        for (int i = 0; i < KH; i += 4) {
             const int k = kof(j, i);
             const float* pr = w_hh + (size_t)uf * H + k;
             const float* pz = pr + (size_t)H * H;
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
                 const float4 a = ok ? *reinterpret_cast<const float4*>(pr) : z4;
                 const float4 b = ok ? *reinterpret_cast<const float4*>(pz) : z4;
                 const float4 c = ok ? *reinterpret_cast<const float4*>(pn) : z4;
-                const int e = 8 * j + i;
+                const int e = KH * j + i;
                 wr[e] = a.x; wr[e + 1] = a.y; wr[e + 2] = a.z; wr[e + 3] = a.w;
                 wz[e] = b.x; wz[e + 1] = b.y; wz[e + 2] = b.z; wz[e + 3] = b.w;
                 wn[e] = c.x; wn[e + 1] = c.y; wn[e + 2] = c.z; wn[e + 3] = c.w;
@@ -209,9 +212,9 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const bool ok = ufvalid && k + c < H;
-                    wr[8 * j + i + c] = ok ? pr[c] : 0.f;
-                    wz[8 * j + i + c] = ok ? pz[c] : 0.f;
-                    wn[8 * j + i + c] = ok ? pn[c] : 0.f;
+                    wr[KH * j + i + c] = ok ? pr[c] : 0.f;
+                    wz[KH * j + i + c] = ok ? pz[c] : 0.f;
+                    wn[KH * j + i + c] = ok ? pn[c] : 0.f;
                 }
             }
         }
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
     // every row; other lanes, and lanes of a k past H, re-read the wave's
     // first valid remote word (word 0 when it has none); a row past B reads
     // the group's first row.
-    auto pkof = [&](int l) { return kofh(l / NP, 1 + (l % NP) / 8, l % 8); };
+    auto pkof = [&](int l) { return kofh(l / NP, 1 + (l % NP) / KH, l % KH); };
     int fallback = -1;
 #pragma unroll
     for (int l = 0; l < 2 * NP * (NR > 0); ++l) {
@@ -287,13 +290,13 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
     // one, which keeps that variant within 256 VGPRs (no scratch).
     constexpr int NACC = R == 4 ? 1 : 2;
     float ar[R][NACC], az[R][NACC], an[R][NACC];
-    // slot j's FMAs of row r with its eight h values (wave-uniform)
-    auto fma8 = [&](const float (&hv)[8], int j, int r) {
+    // slot j's FMAs of row r with its KH h values (wave-uniform)
+    auto fma8 = [&](const float (&hv)[KH], int j, int r) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            ar[r][i % NACC] = fmaf(hv[i], wr[8 * j + i], ar[r][i % NACC]);
-            az[r][i % NACC] = fmaf(hv[i], wz[8 * j + i], az[r][i % NACC]);
-            an[r][i % NACC] = fmaf(hv[i], wn[8 * j + i], an[r][i % NACC]);
+        for (int i = 0; i < KH; ++i) {
+            ar[r][i % NACC] = fmaf(hv[i], wr[KH * j + i], ar[r][i % NACC]);
+            az[r][i % NACC] = fmaf(hv[i], wz[KH * j + i], az[r][i % NACC]);
+            an[r][i % NACC] = fmaf(hv[i], wn[KH * j + i], an[r][i % NACC]);
         }
     };
     auto zero_acc = [&](int r) {
@@ -306,19 +309,20 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
         else
             return a[0];
     };
-    // eight consecutive floats of LDS as wave-uniform values
-    auto lds8 = [](const float* src, float (&hv)[8]) {
-        const float4 a = *reinterpret_cast<const float4*>(src);
-        const float4 b = *reinterpret_cast<const float4*>(src + 4);
-        hv[0] = a.x; hv[1] = a.y; hv[2] = a.z; hv[3] = a.w;
-        hv[4] = b.x; hv[5] = b.y; hv[6] = b.z; hv[7] = b.w;
+    // KH consecutive floats of LDS as wave-uniform values
+    auto lds8 = [](const float* src, float (&hv)[KH]) {
+#pragma unroll
+        for (int q = 0; q < KH; q += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(src + q);
+            hv[q] = a.x; hv[q + 1] = a.y; hv[q + 2] = a.z; hv[q + 3] = a.w;
+        }
     };
     auto local_fmas = [&](int par) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             zero_acc(r);
-            float hl[8];
-            lds8(&hloc[par][r][16 * Q + 8 * hf], hl);
+            float hl[KH];
+            lds8(&hloc[par][r][KP * Q + KH * hf], hl);
             fma8(hl, 0, r);
         }
     };
@@ -329,9 +333,9 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         zero_acc(r);
-        float hv[8];
+        float hv[KH];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < KH; ++i) {
             const int k = kof(0, i);
             hv[i] = k < H && rvalid[r] ? h0[roff[r] + k] : 0.f;
         }
@@ -370,10 +374,10 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
         }
         // with one row, its h values are read ahead of the owner's memory
         // operations
-        float hv0[NR > 0 ? NR : 1][8];
+        float hv0[NR > 0 ? NR : 1][KH];
         if constexpr (R == 1) {
 #pragma unroll
-            for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][8 * jj], hv0[jj]);
+            for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][KH * jj], hv0[jj]);
         }
         if (owner) {
             if (!IO && t > 0) store_outputs(t - 1);
@@ -386,7 +390,7 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
             constexpr bool by_slot = R == 4 && S == 4;
             if constexpr (R > 1 && !by_slot) {
 #pragma unroll
-                for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][8 * jj], hv0[jj]);
+                for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][KH * jj], hv0[jj]);
             }
             if constexpr (!by_slot) {
 #pragma unroll
@@ -399,16 +403,16 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
 #pragma unroll
                     for (int jj = 0; jj < NR; ++jj) {
                         __builtin_amdgcn_sched_barrier(0);
-                        float hv[8];
-                        lds8(&hrem[wave][r][hf][8 * jj], hv);
+                        float hv[KH];
+                        lds8(&hrem[wave][r][hf][KH * jj], hv);
                         fma8(hv, jj + 1, r);
                     }
                 } else {
                     // one row's h values at a time (registers)
                     __builtin_amdgcn_sched_barrier(0);
-                    float hv[NR][8];
+                    float hv[NR][KH];
 #pragma unroll
-                    for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][r][hf][8 * jj], hv[jj]);
+                    for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][r][hf][KH * jj], hv[jj]);
 #pragma unroll
                     for (int jj = 0; jj < NR; ++jj) fma8(hv[jj], jj + 1, r);
                 }
@@ -431,8 +435,11 @@ __global__ __launch_bounds__(IO ? NTH + 64 : NTH) void gru_fwd_local_kernel(
         if (owner) {
             const int pb = t & 1, wr_ = wave;
             auto tree4 = [&](int g) {
-                return (part[pb][0][g][wr_][lane] + part[pb][1][g][wr_][lane]) +
-                       (part[pb][2][g][wr_][lane] + part[pb][3][g][wr_][lane]);
+                if constexpr (NQ == 8)
+                    return rec::tree8([&](int q) { return part[pb][q][g][wr_][lane]; });
+                else
+                    return (part[pb][0][g][wr_][lane] + part[pb][1][g][wr_][lane]) +
+                           (part[pb][2][g][wr_][lane] + part[pb][3][g][wr_][lane]);
             };
             const float sr = bias_r + tree4(0);
             const float sz = bias_z + tree4(1);
@@ -1314,6 +1321,14 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
 }
 
 // ------------------------------------------------------------- config ---
+// Compute wavefronts of the one-row forward: sixteen at four slices (every
+// wave has half the FMAs of eight, and the owner stores its own outputs: a
+// workgroup holds at most 1024 threads), else eight plus the I/O wavefront.
+// Measured on MI355X (same box, alternating runs, forward per launch): c2
+// 434-437 vs 443 us; at one to three slices the I/O wavefront wins (H = 64,
+// 128, 192: 359 / 365 / 403 vs 370 / 389 / 427 us).
+constexpr int fwd_waves1(int S) { return S == 4 ? 16 : 8; }
+
 template <int S>
 const void* local_ptr(int dir, int rows, bool io) {
     if (dir == 1) {
@@ -1326,25 +1341,26 @@ const void* local_ptr(int dir, int rows, bool io) {
     switch (rows) {
         case 1:
             return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true>)
-                      : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false>);
+                      : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false, fwd_waves1(S)>);
         case 2: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 2, false>);
         default: return reinterpret_cast<const void*>(&gru_fwd_mfma4_kernel<S>);
     }
 }
 
-// Whether the kernel for (dir, rows) has the I/O wavefront: the forward
-// with one row per workgroup.
-bool uses_io(int dir, int rows) { return dir == 0 && rows == 1; }
+// Whether the kernel for (dir, rows, slices) has the I/O wavefront: the
+// forward with one row per workgroup and eight compute wavefronts.
+bool uses_io(int dir, int rows, int slices) { return dir == 0 && rows == 1 && fwd_waves1(slices) == 8; }
 
-int block_threads(int dir, int rows) {
+int block_threads(int dir, int rows, int slices) {
     if (dir == 1 && rows == 1) return 16 * 64;  // the one-row backward: sixteen wavefronts
-    return uses_io(dir, rows) ? NTH + 64 : NTH;
+    if (dir == 0 && rows == 1) return fwd_waves1(slices) * 64 + (uses_io(dir, rows, slices) ? 64 : 0);
+    return NTH;
 }
 
 // The local-slice kernels: S slices, 1, 2 or 4 batch rows per workgroup.
 const void* kernel_ptr(int dir, int cap, int rows, int slices) {
     (void)cap;
-    const bool io = uses_io(dir, rows);
+    const bool io = uses_io(dir, rows, slices);
     switch (slices) {
         case 1: return local_ptr<1>(dir, rows, io);
         case 2: return local_ptr<2>(dir, rows, io);
@@ -1390,7 +1406,7 @@ int reg_choose(int dir, int batch, int hidden, const DeviceInfo& dev, int fixed_
         if (rows > max_rows(dir, S) || (fixed_rows && rows != fixed_rows)) continue;
         const int G = (batch + rows - 1) / rows;
         int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows, S), block_threads(dir, rows),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr(dir, cap, rows, S), block_threads(dir, rows, S),
                                                          0) != hipSuccess)
             continue;
         const long resident = (long)per_cu * dev.num_cus;
@@ -1429,12 +1445,12 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     if (dir == 0) {
         void* args[] = {(void*)&a.gx, (void*)&a.h0, (void*)&a.w_hh, (void*)&a.b_hh, (void*)&a.y, (void*)&a.hn,
                         (void*)&a.reserve, (void*)&a.exch, (void*)&a.abort_flag, (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(block_threads(dir, c.rows)), args, 0, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(block_threads(dir, c.rows, c.slices)), args, 0, stream));
     } else {
         void* args[] = {(void*)&a.dy, (void*)&a.dhn, (void*)&a.reserve, (void*)&a.h0, (void*)&a.y,
                         (void*)&a.w_hh, (void*)&a.gout, (void*)&a.dh0, (void*)&a.exch, (void*)&a.abort_flag,
                         (void*)&prm};
-        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(block_threads(dir, c.rows)), args, 0, stream));
+        RKA_RETURN_IF_HIP(hipLaunchKernel(k, dim3(blocks), dim3(block_threads(dir, c.rows, c.slices)), args, 0, stream));
     }
     return 0;
 }

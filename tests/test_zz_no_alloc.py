@@ -82,7 +82,7 @@ def test_noalloc_forward_rejects_shapes_beyond_its_static_scratch(gpu, hip_lib):
     assert rc == 1004  # RKA_ERR_UNSUPPORTED_SHAPE
     assert "static scratch limit" in _lib.last_error()
     # step tags carry a call number in their top 8 bits: seq_len < 2^24
-    rc = hip_lib.rka_gru_recurrence_forward_noalloc(p, p, p, p, p, p, None, 4, 1 << 24, 64,
+    rc = hip_lib.rka_gru_recurrence_forward_noalloc(p, p, p, p, p, p, None, 1, 1 << 24, 16,
                                                     torch.cuda.current_stream().cuda_stream)
     assert rc == 1004
     assert "2^24" in _lib.last_error()
