@@ -6,12 +6,15 @@
 //   weight gradients  dW  = G^T [X | Hprev]        (A k-major,  B k-major)
 // C[m,n] = sum_k A(m,k) B(n,k).  A workgroup of 4 wavefronts computes a
 // 128x128 tile; each wavefront owns a 64x64 quadrant as 4x4 MFMA 16x16
-// blocks; three workgroups per CU.  Interior tiles load their 16-deep
-// operand tiles straight from global memory into a three-stage LDS ring
-// (global_load_lds_dwordx4); edge tiles and operands that are not 16-byte
-// aligned stage them through registers into double-buffered LDS (bounds-
-// checked loads as range-checked buffer loads; unaligned operands one float
-// per lane, in kernel instances of their own).  The LDS
+// blocks; three workgroups per CU.  Tiles of 16-byte aligned operands load
+// their 16-deep operand tiles straight from global memory into a three-stage
+// LDS ring (global_load_lds_dwordx4); edge tiles clamp those loads to the
+// operand's last row, and a k extent that is not a multiple of 16 ends with
+// one k-tile read through registers into the same ring.  Operands that are
+// not 16-byte aligned stage their tiles through registers into double-
+// buffered LDS (range-checked buffer loads, one float per lane, in kernel
+// instances of their own).  In an edge tile, a wavefront whose 64x64
+// quadrant holds no output issues no MFMAs.  The LDS
 // forms are chosen so that every MFMA operand read is one conflict-free
 // ds_read_b128 feeding four MFMAs: a k-major tile is kept [k][row] (a lane
 // reads four rows at one k), a row-major one [row][k] (four k of one row;
@@ -425,7 +428,7 @@ __device__ __forceinline__ void mma_tile(const float* as, const float* bs, int l
 // otherwise both operands take the float4 loads, and the one-float-per-lane
 // code, whose addresses would hold ~40 more VGPRs and cost the aligned
 // kernels their third workgroup per CU, is not compiled in.
-template <int AK, int BKM, bool BSHIFT, bool SEG, int BK, bool UA>
+template <int AK, int BKM, bool BSHIFT, bool SEG, int BK, bool UA, bool IDLE = false>
 __device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int nkb,
                                                  int tid, int lane, int wm, int wn, bool colsum, float& cs,
                                                  float* As0, float* As1, float* Bs0, float* Bs1,
@@ -450,7 +453,7 @@ __device__ __forceinline__ void mainloop(const GemmArgs& p, int m0, int n0, int 
             load_tile<AK, false, SEG, BK>(p.a, av, p.m, kend, m0, kbeg + (kb + 1) * BK, tid, ra);
             load_tile<BKM, BSHIFT, SEG, BK>(p.b, bv, p.n, kend, n0, kbeg + (kb + 1) * BK, tid, rb);
         }
-        mma_tile<AK, BK>(as, bs, lane, wm, wn, tid, colsum, cs, acc);
+        if constexpr (!IDLE) mma_tile<AK, BK>(as, bs, lane, wm, wn, tid, colsum, cs, acc);
         if (more) {
             store_tile<AK, AK, BK>(as_n, tid, av, ra);
             store_tile<BKM, 1, BK>(bs_n, tid, bv, rb);
@@ -501,16 +504,24 @@ constexpr int kDmaTile = 16 * BM;  // floats per operand tile
 //     4-bank groups.  (rocprofv3 counts 4 bank-conflict cycles per such
 //     read; a swizzle that also spreads every 8-lane group over 128 bytes
 //     left that count and the run time unchanged.)
-// R: rows of the tile (k form: R / 4 chunks per k row).
-template <int KMAJOR, bool SHIFT, bool SEG, bool ROT, int R = BM>
-__device__ __forceinline__ const float* dma_src(const GemmOperand& op, int r0, int k0, int s) {
+// R: rows of the tile (k form: R / 4 chunks per k row).  CLAMP (edge
+// tiles): a chunk past the operand's last row reads the last row (k form:
+// the last four, `rows` being a multiple of 4 there), so every load stays
+// inside the operand; the products of those rows land in outputs that are
+// not stored.
+template <int KMAJOR, bool SHIFT, bool SEG, bool ROT, int R = BM, bool CLAMP = false>
+__device__ __forceinline__ const float* dma_src(const GemmOperand& op, int r0, int k0, int s, int rows = 0) {
     if constexpr (KMAJOR == 1) {
-        return elem_ptr<1, SHIFT, SEG>(op, r0 + 4 * (s % (R / 4)), k0 + s / (R / 4));
+        int r = r0 + 4 * (s % (R / 4));
+        if constexpr (CLAMP) r = min(r, rows - 4);
+        return elem_ptr<1, SHIFT, SEG>(op, r, k0 + s / (R / 4));
     } else {
         const int t = s >> 2;
         const int kq = (s & 3) ^ ((t >> 2) & 3);
         const int row = ROT ? (t & ~63) | ((t & 15) << 2) | ((t >> 4) & 3) : t;
-        return elem_ptr<0, false, SEG>(op, r0 + row, k0 + 4 * kq);
+        int r = r0 + row;
+        if constexpr (CLAMP) r = min(r, rows - 1);
+        return elem_ptr<0, false, SEG>(op, r, k0 + 4 * kq);
     }
 }
 
@@ -538,21 +549,60 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     }
 }
 
-template <int AK, int BKM, bool BSHIFT, bool SEG>
-__device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, int kbeg, int nkb, int tid, int lane,
+// A last k-tile of fewer than 16 (k extent or split chunk not a multiple of
+// 16) takes the same ring stage and LDS form: its chunks are read with
+// bounds-checked float4 loads (zero past kend) and written with
+// ds_write_b128 where the DMA would have put them, so every k-tile meets
+// the same MFMA code.  Edge tiles clamp their loads (dma_src).  IDLE: a
+// wavefront whose 64x64 quadrant holds no output issues its share of the
+// loads and the barriers but no MFMAs.
+template <int AK, int BKM, bool BSHIFT, bool SEG, bool IDLE = false>
+__device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, int kbeg, int kend, int tid, int lane,
                                              int wm, int wn, bool colsum, float& cs, float* smem,
                                              floatx4 (&acc)[4][4]) {
     const int wave = tid >> 6;
+    const int nkw = (kend - kbeg) / 16;                 // whole k-tiles
+    const int nkb = (kend - kbeg + 15) / 16;            // with the short last one
     auto a_stage = [&](int st) { return smem + st * 2 * kDmaTile; };
     auto b_stage = [&](int st) { return smem + st * 2 * kDmaTile + kDmaTile; };
     auto issue = [&](int kb, int st) {
         const int k0 = kbeg + kb * 16;
+        if (kb < nkw) {
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const int s0 = 64 * (2 * wave + d);  // first chunk of this wave's 1 KB block
+                lds_dma16(dma_src<AK, false, SEG, false, BM, true>(p.a, m0, k0, s0 + lane, p.m),
+                          a_stage(st) + 4 * s0);
+                lds_dma16(dma_src<BKM, BSHIFT, SEG, true, BM, true>(p.b, n0, k0, s0 + lane, p.n),
+                          b_stage(st) + 4 * s0);
+            }
+            return;
+        }
+        // the short last k-tile: chunk s of a k-major operand is k row s / 32,
+        // of a row-major one k quad kq (dma_src's swizzle); a chunk past kend
+        // is zero (k extents of row-major float4 operands are multiples of 4)
+        float4 v[4];
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
-            const int s0 = 64 * (2 * wave + d);  // first chunk of this wave's 1 KB block
-            lds_dma16(dma_src<AK, false, SEG, false>(p.a, m0, k0, s0 + lane), a_stage(st) + 4 * s0);
-            lds_dma16(dma_src<BKM, BSHIFT, SEG, true>(p.b, n0, k0, s0 + lane), b_stage(st) + 4 * s0);
+            const int sc = 64 * (2 * wave + d) + lane;
+            const int ka = AK == 1 ? k0 + sc / 32 : k0 + 4 * ((sc & 3) ^ ((sc >> 4) & 3));
+            const int kb2 = BKM == 1 ? k0 + sc / 32 : k0 + 4 * ((sc & 3) ^ ((sc >> 4) & 3));
+            v[2 * d] = ka < kend ? *reinterpret_cast<const float4*>(
+                                       dma_src<AK, false, SEG, false, BM, true>(p.a, m0, k0, sc, p.m))
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[2 * d + 1] = kb2 < kend ? *reinterpret_cast<const float4*>(
+                                            dma_src<BKM, BSHIFT, SEG, true, BM, true>(p.b, n0, k0, sc, p.n))
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+        // the ring's DMA loads are counted on the same counter: wait for all
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const int s0 = 64 * (2 * wave + d);
+            *reinterpret_cast<float4*>(a_stage(st) + 4 * (s0 + lane)) = v[2 * d];
+            *reinterpret_cast<float4*>(b_stage(st) + 4 * (s0 + lane)) = v[2 * d + 1];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
     for (int kb = 0; kb < kDmaStages - 1 && kb < nkb; ++kb) issue(kb, kb);
     for (int kb = 0; kb < nkb; ++kb) {
@@ -571,12 +621,12 @@ __device__ __forceinline__ void mainloop_dma(const GemmArgs& p, int m0, int n0, 
         auto refill = [&]() {
             if (kb + kDmaStages - 1 < nkb) issue(kb + kDmaStages - 1, (kb + kDmaStages - 1) % kDmaStages);
         };
-        if constexpr (AK == 1) refill();
-        mma_tile<AK == 1 ? 1 : 2, 16, BM, BKM == 1 ? 1 : 2>(a_stage(kb % kDmaStages), b_stage(kb % kDmaStages), lane,
-                                                           wm, wn, tid, colsum, cs, acc,
-                                                           [&]() {
-                                                               if constexpr (AK == 0) refill();
-                                                           });
+        if constexpr (AK == 1 || IDLE) refill();
+        if constexpr (!IDLE)
+            mma_tile<AK == 1 ? 1 : 2, 16, BM, BKM == 1 ? 1 : 2>(a_stage(kb % kDmaStages), b_stage(kb % kDmaStages),
+                                                               lane, wm, wn, tid, colsum, cs, acc, [&]() {
+                                                                   if constexpr (AK == 0) refill();
+                                                               });
     }
 }
 
@@ -674,11 +724,26 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int bx, int by, int
         for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
     float cs = 0.f;
 
-    if (kDma && p.a_vec && p.b_vec && m0 + BM <= p.m && n0 + BN <= p.n && nkb > 0 && (kend - kbeg) % BK == 0)
-        mainloop_dma<AK, BKM, BSHIFT, SEG>(p, m0, n0, kbeg, nkb, tid, lane, wm, wn, colsum, cs, smem, acc);
-    else
+    // an edge tile's wavefront whose 64x64 quadrant holds no output loads its
+    // share of the operand tiles for the others and issues no MFMAs (its rows
+    // are past p.m, so it has no column sums to store either)
+    const bool idle = m0 + 64 * wm >= p.m || n0 + 64 * wn >= p.n - p.narrow;
+    if (kDma && (!UA || (p.a_vec && p.b_vec))) {
+        // both operands float4-capable (always so in the aligned instances)
+        if (idle) {
+            mainloop_dma<AK, BKM, BSHIFT, SEG, true>(p, m0, n0, kbeg, kend, tid, lane, wm, wn, false, cs, smem, acc);
+            return;
+        }
+        mainloop_dma<AK, BKM, BSHIFT, SEG>(p, m0, n0, kbeg, kend, tid, lane, wm, wn, colsum, cs, smem, acc);
+    } else {
+        if (idle) {
+            mainloop<AK, BKM, BSHIFT, SEG, BK, UA, true>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, false, cs, As0,
+                                                         As1, Bs0, Bs1, acc);
+            return;
+        }
         mainloop<AK, BKM, BSHIFT, SEG, BK, UA>(p, m0, n0, kbeg, kend, nkb, tid, lane, wm, wn, colsum, cs, As0, As1, Bs0,
                                            Bs1, acc);
+    }
     store_c<AK, SPLIT, SEG>(p, m0, n0, bz, wm, wn, lane, acc);
     if (colsum && tid < BM && m0 + tid < p.m) {
         float* cpart = p.partial + (size_t)p.ksplit_total * p.m * p.n;
