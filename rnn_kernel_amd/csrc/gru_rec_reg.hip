@@ -231,7 +231,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
         for (int c = 0; c < 3; ++c) gxs[e][c] = 0.f;
     const float* gx_row = gx + (size_t)orow * T * 3 * H + u;
     auto load_gx = [&](float (&d)[3], int t) {
-        const float* gp = gx_row + (size_t)t * 3 * H;
+        const float* gp = gx_row + (unsigned)t * (unsigned)(3 * H);  // 32-bit: B T H < 2^29
         d[0] = gp[0];
         d[1] = gp[H];
         d[2] = gp[2 * H];
@@ -281,8 +281,8 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
     float* y_row = y + (size_t)orow * T * H + u;
     float* res_row = reserve ? reserve + (size_t)orow * T * 4 * H + 4 * u : nullptr;
     auto store_outputs = [&](int t) {
-        y_row[(size_t)t * H] = o_h;
-        if (res_row) *reinterpret_cast<float4*>(res_row + (size_t)t * 4 * H) = make_float4(o_r, o_z, o_n, o_a);
+        y_row[(unsigned)t * (unsigned)H] = o_h;
+        if (res_row) *reinterpret_cast<float4*>(res_row + 4 * ((unsigned)t * (unsigned)H)) = make_float4(o_r, o_z, o_n, o_a);
     };
     // partial sums of the step in flight per row; the own slot's FMAs land
     // first.  Two accumulators per gate and row give each wave six
@@ -944,17 +944,25 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     float dh = 0.f, ddirect = 0.f;
     float o_dan = 0.f, o_drh = 0.f, o_dzh = 0.f, o_dnh = 0.f;
     float ins[2][6];
+    // The owner row's bases are wave-uniform (scalar) and fixed; a step adds
+    // t H, a 32-bit product (B T H < 2^29, checked on the host), so the step
+    // loop carries no 64-bit multiplies.
+    const size_t row_el = (size_t)orow * T * H;
+    const float* dy_r = dy ? dy + row_el : nullptr;
+    const float* res_r = reserve + 4 * row_el;
+    const float* y_r = y + row_el;
+    const float* h0_r = h0 + (size_t)orow * H;
+    float* g_r = gout + 4 * row_el;
     auto load_inputs = [&](float (&d)[6], int t) {
-        // row pointers are wave-uniform (scalar); the unit is the lane offset
-        const size_t bt = (size_t)orow * T + t;
-        d[0] = dy ? (dy + bt * H)[u] : 0.f;
+        const unsigned tH = (unsigned)t * (unsigned)H;
+        d[0] = dy_r ? dy_r[tH + u] : 0.f;
         // the unit's (r, z, n, a_n) as one float4 (reserve [B, T, H, 4])
-        const float4 c4 = *reinterpret_cast<const float4*>(reserve + bt * 4 * H + 4 * u);
+        const float4 c4 = *reinterpret_cast<const float4*>(res_r + 4 * (tH + u));
         d[1] = c4.x;
         d[2] = c4.y;
         d[3] = c4.z;
         d[4] = c4.w;
-        d[5] = t > 0 ? (y + (bt - 1) * H)[u] : (h0 + (size_t)orow * H)[u];
+        d[5] = t > 0 ? y_r[tH - H + u] : h0_r[u];
     };
 #pragma unroll
     for (int e = 0; e < 2; ++e)
@@ -1126,7 +1134,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
             // this kernel, so it need not take MALL space from the reserve,
             // y and dy this kernel still has to read (backward 0.449 vs
             // 0.467 ms per c2 launch, same-box A/B)
-            float* op = gout + ((size_t)orow * T + t) * 4 * H;  // wave-uniform
+            float* op = g_r + 4 * (unsigned)t * (unsigned)H;  // wave-uniform
             __builtin_nontemporal_store(o_dan, op + u);
             __builtin_nontemporal_store(o_drh, op + H + u);
             __builtin_nontemporal_store(o_dzh, op + 2 * H + u);
@@ -1228,7 +1236,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
         }
         // @probe:phase_polled
         if (owner && mine) {
-            float* op = gout + ((size_t)orow * T + t) * 4 * H;  // wave-uniform
+            float* op = g_r + 4 * (unsigned)t * (unsigned)H;  // wave-uniform
             __builtin_nontemporal_store(o_dan, op + u);
             __builtin_nontemporal_store(o_drh, op + H + u);
             __builtin_nontemporal_store(o_dzh, op + 2 * H + u);
