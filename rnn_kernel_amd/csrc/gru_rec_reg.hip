@@ -111,9 +111,15 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
     constexpr int NQ = NWF / 2;               // k parts of a slot (a wave takes one for 32 units)
     constexpr int KP = 64 / NQ, KH = KP / 2;  // k per part, per wave half
     constexpr int NP = NR > 0 ? KH * NR : 4;  // polled h values per wave half and row
-    __shared__ float part[2][NQ][3][R][64];   // [step parity][k part][gate][row][unit]
+    static_assert(2 * NP <= 64, "a wave's polled words fit its 64 LDS entries");
+    // [step parity][k part][gate][row][unit]; gate 3 takes the upper half's
+    // copy of the n sum, so both halves store without a branch
+    __shared__ float part[2][NQ][4][R][64];
     __shared__ __attribute__((aligned(16))) float hloc[2][R][64];
-    __shared__ __attribute__((aligned(16))) float hrem[NWF][R][2][NP];  // per wave, row and half: the polled h values
+    // per wave and row: the polled h values, half h's NP at [h NP, h NP + NP)
+    // (lane l's word at l; lanes past 2 NP write unread entries, so no lane
+    // needs a branch)
+    __shared__ __attribute__((aligned(16))) float hrem[NWF][R][64];
     __shared__ float io_out[IO ? 2 : 1][5][64];  // IO: outputs (h, r, z, n, a_n) of a step, by step parity
     __shared__ int s_abort;
     __shared__ int s_local;
@@ -366,10 +372,8 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
             // lanes 0..NP-1 hold slot 1 + l / 8, entry l % 8 of half 0 (NP..
             // of half 1): through the wave's LDS rows to every lane (one wave
             // writes and reads the rows; LDS keeps a wave's accesses in order)
-            if (lane < 2 * NP) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) hrem[wave][r][lane / NP][lane % NP] = hx[r];
-            }
+            for (int r = 0; r < R; ++r) hrem[wave][r][lane] = hx[r];
             __builtin_amdgcn_wave_barrier();
         }
         // with one row, its h values are read ahead of the owner's memory
@@ -377,7 +381,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
         float hv0[NR > 0 ? NR : 1][KH];
         if constexpr (R == 1) {
 #pragma unroll
-            for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][KH * jj], hv0[jj]);
+            for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][NP * hf + KH * jj], hv0[jj]);
         }
         if (owner) {
             if (!IO && t > 0) store_outputs(t - 1);
@@ -390,7 +394,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
             constexpr bool by_slot = R == 4 && S == 4;
             if constexpr (R > 1 && !by_slot) {
 #pragma unroll
-                for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][hf][KH * jj], hv0[jj]);
+                for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][0][NP * hf + KH * jj], hv0[jj]);
             }
             if constexpr (!by_slot) {
 #pragma unroll
@@ -404,7 +408,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
                     for (int jj = 0; jj < NR; ++jj) {
                         __builtin_amdgcn_sched_barrier(0);
                         float hv[KH];
-                        lds8(&hrem[wave][r][hf][KH * jj], hv);
+                        lds8(&hrem[wave][r][NP * hf + KH * jj], hv);
                         fma8(hv, jj + 1, r);
                     }
                 } else {
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
                     __builtin_amdgcn_sched_barrier(0);
                     float hv[NR][KH];
 #pragma unroll
-                    for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][r][hf][KH * jj], hv[jj]);
+                    for (int jj = 0; jj < NR; ++jj) lds8(&hrem[wave][r][NP * hf + KH * jj], hv[jj]);
 #pragma unroll
                     for (int jj = 0; jj < NR; ++jj) fma8(hv[jj], jj + 1, r);
                 }
@@ -426,7 +430,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
             const auto prz = __builtin_amdgcn_permlane32_swap(__float_as_uint(r0), __float_as_uint(z0), false, false);
             const auto pn = __builtin_amdgcn_permlane32_swap(__float_as_uint(n0), __float_as_uint(n0), false, false);
             part[t & 1][Q][hf][r][fu] = __uint_as_float(prz[0]) + __uint_as_float(prz[1]);
-            if (hf == 0) part[t & 1][Q][2][r][fu] = __uint_as_float(pn[0]) + __uint_as_float(pn[1]);
+            part[t & 1][Q][2 + hf][r][fu] = __uint_as_float(pn[0]) + __uint_as_float(pn[1]);
         }
         // @probe:computed
         __syncthreads();
