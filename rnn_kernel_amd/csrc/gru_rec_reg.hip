@@ -98,7 +98,7 @@ struct RegParams {
 // wavefront (registers or LDS-DMA, one to three steps ahead) measured 0.53
 // to 0.57 ms, while the same copies from L2-resident addresses measured
 // 0.455 ms.
-template <int S, int R, bool IO, int NWF = NW>
+template <int S, int R, bool IO, int NWF = NW, bool FULL = false>
 __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_kernel(
     const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
     const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
@@ -124,15 +124,18 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
     __shared__ int s_abort;
     __shared__ int s_local;
 
-    const int B = p.B, T = p.T, H = p.H;
+    // FULL: H = 64 S (every slice whole), a compile-time constant; every
+    // lane's unit exists, so the owner test is the same for the whole
+    // wavefront and its branches need no lane masks
+    const int B = p.B, T = p.T, H = FULL ? 64 * S : p.H;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = FULL ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : threadIdx.x >> 6;
     const rec::GroupCoords gc = rec::group_coords(p.S);
     if (gc.g >= p.G) return;  // padding workgroup of a grid rounded up to whole XCDs
     const int s = gc.s;
     const int row0 = gc.g * R;    // the group's first batch row
     const int u = s * 64 + lane;  // the owner lane's unit
-    const bool uvalid = u < H;
+    const bool uvalid = FULL || u < H;
     // FMA layout: wave w takes units 32 (w / NQ) + l % 32 of the slice and k
     // part Q = w % NQ; half hf = l / 32 of the wave the KH k
     // 64 ((s + j) mod S) + KP Q + KH hf + i of slot j (for every row)
@@ -856,7 +859,7 @@ __device__ __forceinline__ float rows_transpose_sum(const float (&t)[4]) {
 // wavefronts issue the same instructions per SIMD; measured at c2 (same
 // box, three pairs) the one-row backward took 444.2-447.0 vs 447.5-448.4
 // us per launch and the step 1.355-1.358 vs 1.361-1.364 ms.
-template <int S, int R, int NWB = NW, int PH = 1>
+template <int S, int R, int NWB = NW, int PH = 1, bool FULL = false>
 __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     const float* __restrict__ dy, const float* __restrict__ dhn, const float* __restrict__ reserve,
     const float* __restrict__ h0, const float* __restrict__ y, const float* __restrict__ w_hh,
@@ -879,7 +882,8 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     __shared__ int s_abort2[2];  // two phases per step: by step parity
     __shared__ int s_local;
 
-    const int B = p.B, T = p.T, H = p.H;
+    // FULL: H = 64 S, a compile-time constant, and every lane's unit exists
+    const int B = p.B, T = p.T, H = FULL ? 64 * S : p.H;
     const int H3 = 3 * H;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -888,7 +892,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     const int row0 = gc.g * R;  // the group's first batch row
     const int s = gc.s;
     const int u = s * 64 + lane;  // the owner lane's unit
-    const bool uvalid = u < H;
+    const bool uvalid = FULL || u < H;
     const int i0 = T - p.t_end, i1 = T - p.t_begin;  // steps i0 .. i1-1 (t = T-1-i)
 
     const int rho = lane >> 4, q = lane & 15;
@@ -1342,8 +1346,10 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
 constexpr int fwd_waves1(int S) { return S == 4 ? 16 : 8; }
 
 template <int S>
-const void* local_ptr(int dir, int rows, bool io) {
+const void* local_ptr(int dir, int rows, bool io, bool full) {
     if (dir == 1) {
+        if (full && rows == 1) return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 1, 16, 1, true>);
+        if (full && rows == 4) return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 4, NW, 2, true>);
         switch (rows) {
             case 1: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 1, 16>);
             case 2: return reinterpret_cast<const void*>(&gru_bwd_local_kernel<S, 2>);
@@ -1352,6 +1358,9 @@ const void* local_ptr(int dir, int rows, bool io) {
     }
     switch (rows) {
         case 1:
+            if (full)
+                return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true, NW, true>)
+                          : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false, fwd_waves1(S), true>);
             return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true>)
                       : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false, fwd_waves1(S)>);
         case 2: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 2, false>);
@@ -1370,14 +1379,15 @@ int block_threads(int dir, int rows, int slices) {
 }
 
 // The local-slice kernels: S slices, 1, 2 or 4 batch rows per workgroup.
-const void* kernel_ptr(int dir, int cap, int rows, int slices) {
+// full: H = 64 * slices (the one-row forward has instances for it).
+const void* kernel_ptr(int dir, int cap, int rows, int slices, bool full = false) {
     (void)cap;
     const bool io = uses_io(dir, rows, slices);
     switch (slices) {
-        case 1: return local_ptr<1>(dir, rows, io);
-        case 2: return local_ptr<2>(dir, rows, io);
-        case 3: return local_ptr<3>(dir, rows, io);
-        default: return local_ptr<4>(dir, rows, io);
+        case 1: return local_ptr<1>(dir, rows, io, full);
+        case 2: return local_ptr<2>(dir, rows, io, full);
+        case 3: return local_ptr<3>(dir, rows, io, full);
+        default: return local_ptr<4>(dir, rows, io, full);
     }
 }
 
@@ -1451,7 +1461,12 @@ int reg_launch(int dir, const RecConfig& c, const rec::Args& a, hipStream_t stre
     RegParams prm{a.B, a.T, a.H, c.groups, c.slices, c.chunk,
                   (aligned && (a.H & 3) == 0 && (c.chunk & 3) == 0) ? 1 : 0, a.t_begin, a.t_end,
                   a.xcc_words, a.xcc_tag, a.tag_base, a.spin_limit, a.abort_count, a.stall_block};
-    const void* k = kernel_ptr(dir, cap, c.rows, c.slices);
+    // whole slices: the forward always takes the compile-time-H instances;
+    // the one-row backward only on grids of 128 or more workgroups (c2: 434
+    // -> 427 us per launch; at 64 workgroups, c5, 3.44 -> 3.54 ms per step)
+    bool full = a.H == 64 * c.slices;
+    if (dir == 1 && c.rows == 1 && (long)c.groups * c.slices < 128) full = false;
+    const void* k = kernel_ptr(dir, cap, c.rows, c.slices, full);
     if (k == nullptr) return fail(RKA_ERR_UNSUPPORTED_SHAPE, "register recurrence: no kernel for this row count");
     const unsigned blocks = (unsigned)(grid_groups(c, c.groups) * c.slices);
     if (dir == 0) {
