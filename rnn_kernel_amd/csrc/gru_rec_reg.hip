@@ -543,7 +543,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
 // and the owner of row r (wavefront r) adds them in a fixed tree.  The
 // exchange, its words and tags, the owners' gate math, outputs and failure
 // handling are those of gru_fwd_local_kernel with four rows.
-template <int S>
+template <int S, bool FULL = false>
 __global__ __launch_bounds__(NTH) void gru_fwd_mfma4_kernel(
     const float* __restrict__ gx, const float* __restrict__ h0, const float* __restrict__ w_hh,
     const float* __restrict__ b_hh, float* __restrict__ y, float* __restrict__ hn,
@@ -560,7 +560,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_mfma4_kernel(
     __shared__ int s_abort;
     __shared__ int s_local;
 
-    const int B = p.B, T = p.T, H = p.H;
+    const int B = p.B, T = p.T, H = FULL ? 64 * S : p.H;  // FULL: whole slices, H a constant
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const rec::GroupCoords gc = rec::group_coords(p.S);
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(NTH) void gru_fwd_mfma4_kernel(
     const int s = gc.s;
     const int row0 = gc.g * R;
     const int u = s * 64 + lane;  // this lane's unit (A row, owner unit)
-    const bool uvalid = u < H;
+    const bool uvalid = FULL || u < H;
     const int lrow = lane & 3;    // this lane's B column / D column: row lrow
     auto kof = [&](int j, int c) { return 64 * ((s + j) % S) + 8 * wave + c; };
 
@@ -1364,7 +1364,9 @@ const void* local_ptr(int dir, int rows, bool io, bool full) {
             return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true>)
                       : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false, fwd_waves1(S)>);
         case 2: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 2, false>);
-        default: return reinterpret_cast<const void*>(&gru_fwd_mfma4_kernel<S>);
+        default:
+            return full ? reinterpret_cast<const void*>(&gru_fwd_mfma4_kernel<S, true>)
+                        : reinterpret_cast<const void*>(&gru_fwd_mfma4_kernel<S>);
     }
 }
 
