@@ -160,7 +160,7 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
             auto store_step = [&](int t, const float (&o)[5]) {
                 if (!valid) return;
                 yp[(size_t)t * H] = o[0];
-                if (rp) *reinterpret_cast<float4*>(rp + (size_t)t * 4 * H) = make_float4(o[1], o[2], o[3], o[4]);
+                if (reserve) *reinterpret_cast<float4*>(rp + (size_t)t * 4 * H) = make_float4(o[1], o[2], o[3], o[4]);
             };
             auto read_out = [&](int t, float (&o)[5]) {
 #pragma unroll
@@ -291,7 +291,9 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
     float* res_row = reserve ? reserve + (size_t)orow * T * 4 * H + 4 * u : nullptr;
     auto store_outputs = [&](int t) {
         y_row[(unsigned)t * (unsigned)H] = o_h;
-        if (res_row) *reinterpret_cast<float4*>(res_row + 4 * ((unsigned)t * (unsigned)H)) = make_float4(o_r, o_z, o_n, o_a);
+        // the test on the kernel argument is wave-uniform (a per-lane pointer's
+        // is not, and costs an exec-mask branch per step)
+        if (reserve) *reinterpret_cast<float4*>(res_row + 4 * ((unsigned)t * (unsigned)H)) = make_float4(o_r, o_z, o_n, o_a);
     };
     // partial sums of the step in flight per row; the own slot's FMAs land
     // first.  Two accumulators per gate and row give each wave six
