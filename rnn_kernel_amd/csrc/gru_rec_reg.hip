@@ -879,7 +879,11 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     constexpr int NW2 = WE > 64 ? 2 : 1;             // poll registers per row
     __shared__ __attribute__((aligned(16))) float part[2][NWB][R][64];
     __shared__ __attribute__((aligned(16))) float gloc[R][NJ][OWN > 4 ? 8 : 4];  // own G words by j-group
-    __shared__ __attribute__((aligned(16))) float grem[NWB][R][4][GR];  // per wave and row: polled words by j-group
+    // per wave and row: polled words by j-group (j-group rho's GR at rho GR),
+    // then 64 entries that lanes without a word write in the two-phase form
+    // instead of branching (c4 backward 4.47 -> 4.36 ms per step; the
+    // one-phase form keeps its branch, which measured no slower)
+    __shared__ __attribute__((aligned(16))) float grem[NWB][R][4 * GR + 64];
     __shared__ int s_abort;
     __shared__ int s_abort2[2];  // two phases per step: by step parity
     __shared__ int s_local;
@@ -1010,6 +1014,11 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     int pidx1 = WE > 64 ? rem_row(WE * wave + 64 + (lane & 7), pv1) : 0;
     if (!pv0) pidx0 = first_any;
     if (!pv1) pidx1 = first1;
+    // where a lane writes its polled words in grem (entry e to j-group e / RE,
+    // position e % RE)
+    constexpr int RE1 = RE > 0 ? RE : 1;
+    const int gslot0 = lane < WE ? (lane / RE1) * GR + lane % RE1 : 4 * GR + lane;
+    const int gslot1 = lane < WE - 64 ? ((64 + lane) / RE1) * GR + (64 + lane) % RE1 : 4 * GR + lane;
     bool rvalid[R];
     int roff[R];  // word offset of row r within a slot (3 B H < 2^31)
 #pragma unroll
@@ -1095,7 +1104,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     auto read_grem = [&](int r, float (&g)[GR]) {
 #pragma unroll
         for (int k = 0; k < GR / 4; ++k) {
-            const float4 v = *reinterpret_cast<const float4*>(&grem[wave][r][rho][4 * k]);
+            const float4 v = *reinterpret_cast<const float4*>(&grem[wave][r][GR * rho + 4 * k]);
             g[4 * k] = v.x;
             g[4 * k + 1] = v.y;
             g[4 * k + 2] = v.z;
@@ -1130,10 +1139,10 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float gr0 = pv[NW2 * r] ? __uint_as_float((unsigned)first_read[NW2 * r]) : 0.f;
-                if (lane < WE) grem[wave][r][lane / RE][lane % RE] = gr0;
+                if (lane < WE) grem[wave][r][gslot0] = gr0;
                 if constexpr (NW2 == 2) {
                     const float gr1 = pv[NW2 * r + 1] ? __uint_as_float((unsigned)first_read[NW2 * r + 1]) : 0.f;
-                    if (lane < WE - 64) grem[wave][r][(64 + lane) / RE][(64 + lane) % RE] = gr1;
+                    if (lane < WE - 64) grem[wave][r][gslot1] = gr1;
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -1235,10 +1244,10 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
             for (int k = 0; k < RP; ++k) {
                 const int r = ra + k;
                 const float gr0 = pv[NW2 * k] ? __uint_as_float((unsigned)fr[NW2 * k]) : 0.f;
-                if (lane < WE) grem[wave][r][lane / RE][lane % RE] = gr0;
+                grem[wave][r][gslot0] = gr0;
                 if constexpr (NW2 == 2) {
                     const float gr1 = pv[NW2 * k + 1] ? __uint_as_float((unsigned)fr[NW2 * k + 1]) : 0.f;
-                    if (lane < WE - 64) grem[wave][r][(64 + lane) / RE][(64 + lane) % RE] = gr1;
+                    grem[wave][r][gslot1] = gr1;
                 }
             }
             __builtin_amdgcn_wave_barrier();
