@@ -443,12 +443,18 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
         const bool abort_now = s_abort != 0;  // read with the partials
         if (owner) {
             const int pb = t & 1, wr_ = wave;
+            // every partial requested before the first add
+            float pq[3][NQ];
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) pq[g][q] = part[pb][q][g][wr_][lane];
+            __builtin_amdgcn_sched_barrier(0);
             auto tree4 = [&](int g) {
                 if constexpr (NQ == 8)
-                    return rec::tree8([&](int q) { return part[pb][q][g][wr_][lane]; });
+                    return rec::tree8([&](int q) { return pq[g][q]; });
                 else
-                    return (part[pb][0][g][wr_][lane] + part[pb][1][g][wr_][lane]) +
-                           (part[pb][2][g][wr_][lane] + part[pb][3][g][wr_][lane]);
+                    return (pq[g][0] + pq[g][1]) + (pq[g][2] + pq[g][3]);
             };
             const float sr = bias_r + tree4(0);
             const float sz = bias_z + tree4(1);
@@ -1186,9 +1192,15 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
         const bool abort_now = s_abort != 0;  // read with the partials
         float tsum = 0.f;
         if (owner) {
-            const float lo = rec::tree8([&](int w2) { return part[i & 1][w2][wave][lane]; });
+            // every partial requested before the first add (one LDS latency
+            // instead of one per half)
+            float pw[NWB];
+#pragma unroll
+            for (int w2 = 0; w2 < NWB; ++w2) pw[w2] = part[i & 1][w2][wave][lane];
+            __builtin_amdgcn_sched_barrier(0);
+            const float lo = rec::tree8([&](int w2) { return pw[w2]; });
             if constexpr (NWB == 16)
-                tsum = lo + rec::tree8([&](int w2) { return part[i & 1][8 + w2][wave][lane]; });
+                tsum = lo + rec::tree8([&](int w2) { return pw[8 + w2]; });
             else
                 tsum = lo;
             dh = ddirect + tsum;
