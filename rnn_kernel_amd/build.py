@@ -11,14 +11,21 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "librnn_kernel_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ["rka_capi.hip", "gemm_f32.hip", "gru_recurrence.hip", "gru_rec_tiled.hip", "gru_rec_reg.hip",
-           "train_ops.hip", "probes.hip"]
+           "gru_rec_bwd1.hip", "train_ops.hip", "probes.hip"]
 ARCH = "gfx950"
+# Flags of single sources on top of compile_flags().  The machine-scheduler
+# strategy is an option per translation unit: the one-row backward's kernels
+# sit in a file of their own to take max-ilp (see that file's header).
+EXTRA_FLAGS = {
+    "gru_rec_bwd1.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
 
 
 def hipcc_path() -> str:
@@ -46,20 +53,38 @@ def compile_flags() -> list:
     ]
 
 
+def _run(cmds: list, verbose: bool) -> None:
+    """Runs the commands concurrently; raises if any fails."""
+    procs = []
+    for cmd in cmds:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    failed = None
+    for proc in procs:
+        out, err = proc.communicate()
+        if proc.returncode != 0 and failed is None:
+            failed = proc.returncode
+            sys.stderr.write(out + err)
+        elif verbose and err.strip():
+            sys.stderr.write(err)
+    if failed is not None:
+        raise RuntimeError(f"hipcc failed with exit code {failed}")
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source (one object each, concurrently) and link the shared
+    library; returns its path."""
     hipcc = hipcc_path()
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc] + compile_flags() + ["-shared", "-o", tmp] + srcs
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
-    if verbose and proc.stderr.strip():
-        sys.stderr.write(proc.stderr)
+    objdir = tempfile.mkdtemp(prefix="rka_build_")
+    try:
+        objs = [os.path.join(objdir, s + ".o") for s in SOURCES]
+        _run([[hipcc] + compile_flags() + EXTRA_FLAGS.get(s, []) + ["-c", os.path.join(CSRC, s), "-o", o]
+              for s, o in zip(SOURCES, objs)], verbose)
+        _run([[hipcc] + compile_flags() + ["-shared", "-o", tmp] + objs], verbose)
+    finally:
+        shutil.rmtree(objdir, ignore_errors=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
