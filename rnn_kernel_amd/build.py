@@ -18,13 +18,15 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "librnn_kernel_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ["rka_capi.hip", "gemm_f32.hip", "gru_recurrence.hip", "gru_rec_tiled.hip", "gru_rec_reg.hip",
-           "gru_rec_bwd1.hip", "train_ops.hip", "probes.hip"]
+           "gru_rec_bwd1.hip", "gru_rec_fwd1.hip", "train_ops.hip", "probes.hip"]
 ARCH = "gfx950"
 # Flags of single sources on top of compile_flags().  The machine-scheduler
-# strategy is an option per translation unit: the one-row backward's kernels
-# sit in a file of their own to take max-ilp (see that file's header).
+# strategy is an option per translation unit: the one-row kernels that
+# measured faster under another strategy sit in files of their own (see
+# their headers).
 EXTRA_FLAGS = {
     "gru_rec_bwd1.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "gru_rec_fwd1.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"],
 }
 
 

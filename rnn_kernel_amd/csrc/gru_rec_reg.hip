@@ -37,9 +37,11 @@ const void* local_ptr(int dir, int rows, bool io, bool full) {
     }
     switch (rows) {
         case 1:
-            if (full)
+            if (full) {
+                if constexpr (S == 4) return rec_fwd1_kernel();
                 return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true, NW, true>)
                           : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false, fwd_waves1(S), true>);
+            }
             return io ? reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, true>)
                       : reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 1, false, fwd_waves1(S)>);
         case 2: return reinterpret_cast<const void*>(&gru_fwd_local_kernel<S, 2, false>);

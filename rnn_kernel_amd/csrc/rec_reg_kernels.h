@@ -1368,5 +1368,8 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
 // translation unit of their own (gru_rec_bwd1.hip), built with its own
 // machine-scheduler strategy.
 const void* rec_bwd1_kernel(int slices);
+// The one-row forward at four whole slices (gru_fwd_local_kernel<4, 1, false,
+// 16, true>, H = 256), likewise (gru_rec_fwd1.hip).
+const void* rec_fwd1_kernel();
 
 }  // namespace rka
