@@ -202,3 +202,18 @@ def test_prod_import_does_not_pull_in_build_tools_or_oracle():
     )
     out = subprocess.run([sys.executable, "-c", script], check=True, env=env, text=True, capture_output=True)
     assert json.loads(out.stdout.strip().splitlines()[-1]) == {"oracle": False, "build": False}
+
+
+def test_build_compiles_every_source_with_the_pool_flags():
+    """Every .hip source under csrc is built; per-file flags name built sources
+    only and add to, never replace, the common flags (packed fp32 ops stay
+    off for every translation unit)."""
+    from rnn_kernel_amd import build as rka_build
+
+    on_disk = sorted(f for f in os.listdir(rka_build.CSRC) if f.endswith(".hip"))
+    assert sorted(rka_build.SOURCES) == on_disk
+    assert set(rka_build.EXTRA_FLAGS) <= set(rka_build.SOURCES)
+    common = rka_build.compile_flags()
+    assert "-packed-fp32-ops" in common and f"--offload-arch={rka_build.ARCH}" in common
+    for flags in rka_build.EXTRA_FLAGS.values():
+        assert all(f not in ("-O0", "-O1", "-O2") and not f.startswith("--offload-arch") for f in flags)
