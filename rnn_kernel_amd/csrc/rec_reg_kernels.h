@@ -47,6 +47,7 @@
 #include "rec_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace rka {
 namespace {
@@ -355,11 +356,13 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
         }
         fma8(hv, 0, r);
     }
-    auto step = [&](int t, const float (&cur)[3], float (&nxt)[3]) -> bool {
+    // first: std::true_type for step 0 (its h values come from h0), else
+    // std::false_type; step 0 runs before the loop, so no later step tests t
+    auto step = [&](auto first, int t, const float (&cur)[3], float (&nxt)[3]) -> bool {
         // @probe:step_begin
         if constexpr (NR > 0) {
             float hx[R];
-            if (t == 0) {
+            if constexpr (decltype(first)::value) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) hx[r] = pvalid && rvalid[r] ? h0[roff[r] + pidx] : 0.f;
             } else {
@@ -372,10 +375,10 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
                     pv[r] = pvalid && rvalid[r];
                 }
                 bool ok = true;
-                rec::wait_words<R, R == 1>(pp, pv, first_read, p.tag_base + (unsigned)t, wc, ok);
+                rec::wait_words<R, R == 1, R == 1>(pp, pv, first_read, p.tag_base + (unsigned)t, wc, ok);
 #pragma unroll
                 for (int r = 0; r < R; ++r) hx[r] = pv[r] ? __uint_as_float((unsigned)first_read[r]) : 0.f;
-                if (!ok) s_abort = 1;
+                if (__builtin_expect(!ok, 0)) s_abort = 1;
             }
             // lanes 0..NP-1 hold slot 1 + l / 8, entry l % 8 of half 0 (NP..
             // of half 1): through the wave's LDS rows to every lane (one wave
@@ -508,14 +511,18 @@ __global__ __launch_bounds__(IO ? NWF * 64 + 64 : NWF * 64) void gru_fwd_local_k
     // step t stores the outputs of step t - 1: after a step that aborts,
     // rows t_stop .. T-1 were not stored
     int t_stop = T;
-    for (int t = 0; t < T; t += 2) {
-        if (!step(t, gxs[0], gxs[1])) {
-            t_stop = t;
-            break;
-        }
-        if (t + 1 < T && !step(t + 1, gxs[1], gxs[0])) {
-            t_stop = t + 1;
-            break;
+    if (T > 0 && !step(std::true_type{}, 0, gxs[0], gxs[1])) {
+        t_stop = 0;
+    } else {
+        for (int t = 1; t < T; t += 2) {
+            if (!step(std::false_type{}, t, gxs[1], gxs[0])) {
+                t_stop = t;
+                break;
+            }
+            if (t + 1 < T && !step(std::false_type{}, t + 1, gxs[0], gxs[1])) {
+                t_stop = t + 1;
+                break;
+            }
         }
     }
     // @probe:kernel_end
