@@ -1129,7 +1129,10 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     };
     // one timestep (i-th from the end): its G words are published and its
     // own-entry FMAs done; false when the workgroup must stop
-    auto step = [&](int i, float (&cur)[6], const float (&nxt)[6]) -> bool {
+    // kind: 3 = at least two steps follow (the next step, and the input loads
+    // two steps ahead, exist), 0 = tested at run time
+    auto step = [&](auto kind, int i, float (&cur)[6], const float (&nxt)[6]) -> bool {
+        constexpr int KIND = decltype(kind)::value;
         // @probe:step_begin
         const int t = T - 1 - i;
         const unsigned long long* slotp = exch + (size_t)(i & 1) * B * H3;
@@ -1174,7 +1177,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
             __builtin_nontemporal_store(o_drh, op + H + u);
             __builtin_nontemporal_store(o_dzh, op + 2 * H + u);
             __builtin_nontemporal_store(o_dnh, op + 3 * H + u);
-            if (t - 2 >= p.t_begin) load_inputs(cur, t - 2);
+            if (KIND == 3 || t - 2 >= p.t_begin) load_inputs(cur, t - 2);
         }
         // @probe:polled
         if constexpr (RE > 0) {
@@ -1215,7 +1218,7 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
                 tsum = lo;
             dh = ddirect + tsum;
         }
-        const bool more = i + 1 < i1;
+        const bool more = KIND == 3 || i + 1 < i1;
         if (more) pointwise(i + 1, nxt, true, tsum);
         // @probe:published
         __syncthreads();
@@ -1325,14 +1328,40 @@ __global__ __launch_bounds__(64 * NWB) void gru_bwd_local_kernel(
     if constexpr (PH == 1) {
         first_poll_rows(i0, 0, R);
         local_fmas_rows(0, R);
-        for (int i = i0; i < i1; i += 2) {
-            if (!step(i, ins[0], ins[1])) {
-                i_stop = i;
-                break;
+        using Bulk = std::integral_constant<int, 3>;
+        using Any = std::integral_constant<int, 0>;
+        // Steps followed by at least two more run without the run-time tests
+        // of the next step and of the loads two steps ahead (the last steps
+        // keep them).  Measured on MI355X (same box, three alternating
+        // pairs): c5 backward 3326-3330 -> 3252-3255 us per launch, H = 128
+        // 346-347 -> 338-340 us; the whole-slice instances at three and four
+        // slices (built with max-ilp) measured slower with it (c2 +5 us) and
+        // keep the single loop.
+        constexpr bool kBulk = !(FULL && S >= 3);
+        int i = i0;
+        if constexpr (kBulk) {
+            // steps i and i + 1 both followed by two more
+            for (; i + 3 < i1; i += 2) {
+                if (!step(Bulk{}, i, ins[0], ins[1])) {
+                    i_stop = i;
+                    break;
+                }
+                if (!step(Bulk{}, i + 1, ins[1], ins[0])) {
+                    i_stop = i + 1;
+                    break;
+                }
             }
-            if (i + 1 < i1 && !step(i + 1, ins[1], ins[0])) {
-                i_stop = i + 1;
-                break;
+        }
+        if (i_stop == i1) {
+            for (; i < i1; i += 2) {
+                if (!step(Any{}, i, ins[0], ins[1])) {
+                    i_stop = i;
+                    break;
+                }
+                if (i + 1 < i1 && !step(Any{}, i + 1, ins[1], ins[0])) {
+                    i_stop = i + 1;
+                    break;
+                }
             }
         }
     } else {
